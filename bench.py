@@ -1,0 +1,192 @@
+#!/usr/bin/env python3
+"""Decode benchmark: 9B-shape qwen35, Q6_K weights, batch-1 greedy decode on one MI355X.
+
+Workload (benchmark config 3): a deterministic synthetic GGUF with the 9B shape (hidden
+4096, 32 layers as [GDN,GDN,GDN,attention] x 8, FFN 12288, vocab 151936, Q6_K
+matrices, random init), a seeded 512-token prompt, then 128 greedy tokens at context
+4096. A "step" is one decoded token. Throughput follows the reference's definition
+(chat.cpp:71, :81): (emitted - 1) / (t_last - t_first), with token completion times from
+HIP events on the backend stream; the prompt prefill is outside the timed region.
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel (by share of step time) from an event-traced eager
+                step: algorithmic bytes per launch / mean launch duration vs 8 TB/s
+  cpu_baseline  the reference CPU path (the C oracle restating it, OpenMP) decoding a
+                bounded sample of the same model on this host's cores
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def model_file(kind: str, seed: int) -> Path:
+    import emprise_amd as ea
+    d = Path(os.environ.get("EMPRISE_BENCH_DIR", tempfile.gettempdir()))
+    path = d / f"emprise_{kind}_seed{seed}.gguf"
+    if not path.exists():
+        t = time.time()
+        tmp = path.with_suffix(".tmp")
+        if kind == "9b_q6k":
+            ea.synth_write(tmp, seed=seed, **ea.NINE_B)
+        elif kind == "9b_q4km":
+            ea.synth_write(tmp, seed=seed, q4_k_m_mix=True, **ea.NINE_B)
+        elif kind == "tiny":
+            ea.synth_write(tmp, seed=seed, **ea.TINY)
+        else:
+            raise ValueError(kind)
+        os.replace(tmp, path)
+        log(f"wrote {path} ({path.stat().st_size / 1e9:.2f} GB) in {time.time() - t:.1f}s")
+    return path
+
+
+def dominant_kernel(trace):
+    """Groups traced launches by kernel; returns the one with the largest total time."""
+    agg = {}
+    for name, nbytes, ms in trace:
+        a = agg.setdefault(name, [0, 0, 0.0])
+        a[0] += 1
+        a[1] += nbytes
+        a[2] += ms
+    name, (launches, nbytes, ms) = max(agg.items(), key=lambda kv: kv[1][2])
+    total_ms = sum(v[2] for v in agg.values())
+    return name, launches, nbytes / launches, ms / launches, ms / total_ms, agg
+
+
+def cpu_baseline(path: Path, seconds: float, context: int):
+    """The reference's OpenMP CPU decode (restated in oracle/) on a bounded sample."""
+    import oracle
+    threads = min(16, os.cpu_count() or 1)  # the reference default, model.cpp:51-52
+    m = oracle.Model(str(path), context=context, threads=threads)
+    import emprise_amd as ea
+    prompt = ea.synth_prompt(0, m.vocab, 4)
+    logits = None
+    for t in prompt:
+        logits = m.evaluate(t)
+    arrivals, tok = [], int(logits.argmax())
+    t0 = time.perf_counter()
+    while True:
+        logits = m.evaluate(tok)
+        tok = int(logits.argmax())
+        arrivals.append(time.perf_counter())
+        if arrivals[-1] - t0 > seconds and len(arrivals) >= 3:
+            break
+    m.close()
+    rate = (len(arrivals) - 1) / (arrivals[-1] - arrivals[0])
+    return {"value": round(rate, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{len(arrivals)} greedy decode steps of the same 9B-shape Q6_K model after a 4-token "
+                      f"prompt (positions 4-{4 + len(arrivals)}), oracle/ C restatement of the reference "
+                      f"CPU path, OpenMP {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=127, help="timed decode steps (tokens after the first)")
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--context", type=int, default=4096)
+    ap.add_argument("--model", default="9b_q6k", choices=["9b_q6k", "9b_q4km", "tiny"])
+    ap.add_argument("--fast-q8", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--trace-steps", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU decode is not part of "
+              "this build", file=sys.stderr)
+        sys.exit(2)
+
+    import emprise_amd as ea
+    path = model_file(args.model, seed=0)
+    t = time.time()
+    model = ea.Model(path, context=args.context, fast_q8=args.fast_q8)
+    info = model.info
+    log(f"loaded {path.name}: {info.weight_bytes / 1e9:.3f} GB on device in {time.time() - t:.1f}s "
+        f"({model.backend_name}); {info.token_weight_bytes / 1e9:.4f} GB streamed per token")
+    prompt = ea.synth_prompt(0, info.vocab, args.prompt)
+
+    # warmup: instantiates the step graphs and touches every weight once
+    model.generate(prompt[:8], max(args.warmup, 2))
+    log("warmup done")
+
+    count = args.steps + 1
+    t0 = time.perf_counter()
+    tokens, arrivals = model.generate(prompt, count)
+    wall = time.perf_counter() - t0
+    if len(tokens) != count:
+        raise RuntimeError(f"generation stopped early ({len(tokens)} of {count} tokens)")
+    decode_s = arrivals[-1] - arrivals[0]
+    value = args.steps / decode_s
+    log(f"prefill {args.prompt} tokens in {arrivals[0]:.3f}s, {args.steps} decode steps in {decode_s:.4f}s "
+        f"-> {value:.1f} tok/s (host wall {wall:.3f}s)")
+
+    # per-kernel timing of eager steps right after the timed region (same positions range)
+    trace = []
+    tok = tokens[-1]
+    for _ in range(args.trace_steps):
+        trace += model.trace_step(tok)
+    name, launches, bpl, mspl, share, agg = dominant_kernel(trace)
+    achieved = bpl / (mspl * 1e-3) / 1e9
+    per_kernel = {k: {"launches": v[0] // args.trace_steps, "ms_per_step": round(v[2] / args.trace_steps, 4),
+                      "GBps": round(v[1] / (v[2] * 1e-3) / 1e9, 1) if v[2] > 0 else None}
+                  for k, v in sorted(agg.items(), key=lambda kv: -kv[1][2])}
+    log(f"dominant kernel {name}: {launches // args.trace_steps} launches/step, {bpl / 1e6:.2f} MB and "
+        f"{mspl * 1e3:.2f} us per launch -> {achieved:.0f} GB/s ({share * 100:.0f}% of traced step time)")
+    log("per kernel: " + json.dumps(per_kernel))
+    model.close()
+
+    e2e_gbs = value * info.token_weight_bytes / 1e9
+    cpu = None
+    if not args.no_cpu and args.model.startswith("9b"):
+        log(f"cpu baseline: ~{args.cpu_seconds:.0f}s sample")
+        cpu = cpu_baseline(path, args.cpu_seconds, args.context)
+        log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
+
+    workload = {"9b_q6k": "9B-shape qwen35 Q6_K greedy decode, batch 1",
+                "9b_q4km": "9B-shape qwen35 Q4_K_M-mix greedy decode, batch 1",
+                "tiny": "tiny qwen35 Q6_K greedy decode, batch 1"}[args.model]
+    line = {
+        "metric": "decode tok/s, 9B-shape Q6_K batch 1, 1xMI355X; % of HBM roofline",
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000.0 / value, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8" if args.fast_q8 else "f32",
+        "data": "synthetic (seeded random-init GGUF and prompt ids)",
+        "config": {"workload": workload + (" (--fast-q8)" if args.fast_q8 else ""), "prompt_tokens": args.prompt,
+                   "generated_tokens": count, "context": args.context, "hidden": info.hidden, "layers": info.layers,
+                   "vocab": info.vocab, "token_weight_bytes": info.token_weight_bytes,
+                   "parallelism": "single GPU"},
+        "hbm_roofline_fraction": round(e2e_gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+                     "bytes_per_launch": int(bpl), "us_per_launch": round(mspl * 1e3, 3),
+                     "launches_per_step": launches // args.trace_steps},
+        "cpu_baseline": cpu,
+        "kernels": per_kernel,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,785 @@
+// C ABI of the gfx950 decode backend (include/emprise_hip.h). Stands in for the
+// reference's CUDA backend (src/cuda.cpp:599-1130) behind emprise::Backend.
+#include "../../include/emprise_hip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+#include "layout.hpp"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+using namespace emprise;
+
+namespace {
+
+thread_local std::string g_error;
+
+emprise_status fail(emprise_status s, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return s;
+}
+
+#define HIP_TRY(expr)                                                                                  \
+    do {                                                                                               \
+        hipError_t e_ = (expr);                                                                        \
+        if (e_ != hipSuccess) return fail(EMPRISE_EDEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+#define TRY(expr)                          \
+    do {                                   \
+        emprise_status s_ = (expr);        \
+        if (s_ != EMPRISE_OK) return s_;   \
+    } while (0)
+
+struct Weight {
+    uint32_t type = 0;
+    uint64_t cols = 0, rows = 0;
+    uint8_t* dev = nullptr;
+    size_t bytes = 0;
+};
+
+bool supported_type(uint32_t t) { return t == kF32 || t == kF16 || t == kBF16 || t == kQ6K || t == kQ4K; }
+
+// Runs f(begin, end) over [0, n) on up to `threads` host threads.
+template <class F> void parallel_rows(uint64_t n, F f) {
+    unsigned threads = std::max(1u, std::min(32u, std::thread::hardware_concurrency()));
+    if (n < 64) threads = 1;
+    std::vector<std::thread> pool;
+    const uint64_t per = (n + threads - 1) / threads;
+    for (unsigned t = 0; t < threads; ++t) {
+        const uint64_t b = t * per, e = std::min(n, b + per);
+        if (b >= e) break;
+        pool.emplace_back([=] { f(b, e); });
+    }
+    for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+struct emprise_hip {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint64_t budget = 0, used = 0;
+    bool q8 = false;
+    bool capturing = false;
+    std::string name;
+    std::unordered_map<uint64_t, Weight> weights;
+    uint64_t next_weight = 1;
+    std::unordered_map<uint64_t, hipGraphExec_t> graphs;
+    uint64_t next_graph = 1;
+    std::vector<hipEvent_t> events;
+    // scratch buffers, grown outside graph capture only
+    struct Scratch {
+        void* ptr = nullptr;
+        size_t bytes = 0;
+    };
+    std::unordered_map<std::string, Scratch> scratch;
+    // kernel trace (emprise_hip_trace_begin/end)
+    struct TraceRec {
+        const char* kernel;
+        uint64_t bytes;
+        hipEvent_t a, b;
+    };
+    bool tracing = false;
+    std::vector<TraceRec> trace;
+    std::vector<hipEvent_t> trace_pool;
+    size_t trace_used = 0;
+
+    hipEvent_t trace_event() {
+        if (trace_used == trace_pool.size()) {
+            hipEvent_t e = nullptr;
+            if (hipEventCreate(&e) != hipSuccess) return nullptr;
+            trace_pool.push_back(e);
+        }
+        return trace_pool[trace_used++];
+    }
+
+    const Weight* weight(uint64_t id) const {
+        auto it = weights.find(id);
+        return it == weights.end() ? nullptr : &it->second;
+    }
+    emprise_status get_scratch(const char* key, size_t bytes, void** out, bool zero = false) {
+        Scratch& s = scratch[key];
+        if (s.bytes < bytes) {
+            if (capturing) return fail(EMPRISE_ESTATE, "scratch '%s' must be sized before graph capture", key);
+            if (s.ptr) HIP_TRY(hipFree(s.ptr));
+            s.ptr = nullptr;
+            s.bytes = 0;
+            HIP_TRY(hipMalloc(&s.ptr, bytes));
+            if (zero) HIP_TRY(hipMemset(s.ptr, 0, bytes));
+            s.bytes = bytes;
+        }
+        *out = s.ptr;
+        return EMPRISE_OK;
+    }
+};
+
+namespace {
+
+emprise_status launched(hipError_t e) {
+    if (e != hipSuccess) return fail(EMPRISE_EDEVICE, "kernel launch: %s", hipGetErrorString(e));
+    return EMPRISE_OK;
+}
+
+// Launches through `launch`; while tracing, brackets it with two events and records the
+// launch's algorithmic bytes.
+template <class F> emprise_status traced(emprise_hip* h, const char* kernel, uint64_t bytes, F launch) {
+    if (!h->tracing) return launched(launch());
+    hipEvent_t a = h->trace_event(), b = h->trace_event();
+    if (!a || !b) return fail(EMPRISE_EDEVICE, "trace event");
+    HIP_TRY(hipEventRecord(a, h->stream));
+    TRY(launched(launch()));
+    HIP_TRY(hipEventRecord(b, h->stream));
+    h->trace.push_back({kernel, bytes, a, b});
+    return EMPRISE_OK;
+}
+
+const char* matvec_name(uint32_t type, bool q8) {
+    switch (type) {
+    case kQ6K: return q8 ? "matvec_q6_k_q8" : "matvec_q6_k";
+    case kQ4K: return "matvec_q4_k";
+    case kF32: return "matvec_f32";
+    case kF16: return "matvec_f16";
+    default: return "matvec_bf16";
+    }
+}
+
+// GDN step: the state is read and written once; q/k/v, gate, alpha, beta read; output written.
+uint64_t gdn_bytes(const GdnArgs& g) {
+    const uint64_t sd = (uint64_t)g.state_dim, vh = (uint64_t)g.value_heads, kh = (uint64_t)g.key_heads;
+    return 2 * vh * sd * sd * 4 + (2 * kh * sd + vh * sd) * 4 + vh * sd * 4 * 2 + vh * 8;
+}
+
+bool is_matrix(const Weight* w) { return w && w->rows >= 1 && w->cols >= 1; }
+
+// Grouped matvec over weights with one input; splits the list into runs of equal type.
+struct Proj {
+    const Weight* w;
+    float* y;
+};
+
+emprise_status run_matvec(emprise_hip* h, const Proj* p, int n, int mode, const emprise_hip_input* in,
+                          const float* x_plain, const float* conv_w, float* conv_state, int conv_width,
+                          unsigned long long* argmax_key) {
+    if (n < 1 || n > kMaxSeg) return fail(EMPRISE_EINVAL, "between 1 and %d projections per call", kMaxSeg);
+    const uint64_t cols = p[0].w->cols;
+    for (int i = 0; i < n; ++i)
+        if (p[i].w->cols != cols) return fail(EMPRISE_EINVAL, "projections sharing an input need equal columns");
+    if (cols > 12288 + 4096) return fail(EMPRISE_EINVAL, "input width %llu exceeds the staged-input limit", (unsigned long long)cols);
+    bool first = true;
+    for (int i = 0; i < n;) {
+        int j = i + 1;
+        if (mode != kMvSwiglu)
+            while (j < n && p[j].w->type == p[i].w->type) ++j;
+        else
+            j = n;
+        const uint32_t type = p[i].w->type;
+        MvArgs a{};
+        a.nseg = j - i;
+        a.cols = (int)cols;
+        a.mode = mode;
+        int g = 0;
+        for (int s = 0; s < a.nseg; ++s) {
+            const Weight* w = p[i + s].w;
+            const int R = (type == kQ6K || type == kQ4K) ? kMvRows : 1;
+            a.seg[s].w = w->dev;
+            a.seg[s].y = p[i + s].y;
+            a.seg[s].rows = (int)w->rows;
+            a.seg[s].g0 = g;
+            if (mode == kMvSwiglu && s == 1) a.seg[s].g0 = 0x7fffffff;
+            else g += (int)((w->rows + R - 1) / R);
+        }
+        a.groups = g;
+        if (in) {
+            a.x = reinterpret_cast<const float*>(in->x);
+            a.delta = reinterpret_cast<const float*>(in->delta);
+            a.x_out = first ? reinterpret_cast<float*>(in->x_out) : nullptr;
+            if (in->norm) {
+                const Weight* nw = h->weight(in->norm);
+                if (!nw || nw->type != kF32 || nw->rows * nw->cols != cols)
+                    return fail(EMPRISE_EINVAL, "norm weight must be F32 with %llu elements", (unsigned long long)cols);
+                a.norm = reinterpret_cast<const float*>(nw->dev);
+            }
+            a.eps = in->eps;
+        } else {
+            a.x = x_plain;
+        }
+        if (first && conv_w) {
+            a.conv_w = conv_w;
+            a.conv_state = conv_state;
+            a.conv_width = conv_width;
+        }
+        a.argmax = argmax_key;
+        const bool q8 = h->q8 && type == kQ6K;
+        // algorithmic bytes: encoded weights + the input read (x, delta, norm) + outputs
+        uint64_t bytes = cols * 4 * (1 + (a.delta ? 1 : 0) + (a.norm ? 1 : 0) + (a.x_out ? 1 : 0));
+        for (int s = 0; s < a.nseg; ++s) bytes += p[i + s].w->bytes + (uint64_t)a.seg[s].rows * 4;
+        if (a.conv_w) bytes += (uint64_t)a.seg[0].rows * a.conv_width * 4 * 3;
+        TRY(traced(h, matvec_name(type, q8), bytes, [&] { return launch_matvec(type, q8, a, 2048, h->stream); }));
+        first = false;
+        i = j;
+    }
+    return EMPRISE_OK;
+}
+
+emprise_status check_weights(emprise_hip* h, int n, const emprise_weight* ids, const Weight** out) {
+    for (int i = 0; i < n; ++i) {
+        out[i] = h->weight(ids[i]);
+        if (!is_matrix(out[i])) return fail(EMPRISE_EINVAL, "unknown weight handle %llu", (unsigned long long)ids[i]);
+    }
+    return EMPRISE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* emprise_hip_last_error(void) { return g_error.c_str(); }
+
+emprise_status emprise_hip_create(int device, uint64_t weight_budget, int quantize_activations, emprise_hip** out) {
+    if (!out) return fail(EMPRISE_EINVAL, "null output");
+    *out = nullptr;
+    int count = 0;
+    HIP_TRY(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return fail(EMPRISE_EINVAL, "no HIP device %d (%d present)", device, count);
+    HIP_TRY(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(EMPRISE_EDEVICE, "built for gfx950, found %s", prop.gcnArchName);
+    auto* h = new emprise_hip();
+    h->device = device;
+    h->q8 = quantize_activations != 0;
+    hipError_t e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete h;
+        return fail(EMPRISE_EDEVICE, "stream: %s", hipGetErrorString(e));
+    }
+    size_t free_b = 0, total_b = 0;
+    (void)hipMemGetInfo(&free_b, &total_b);
+    const uint64_t reserve = 512ull << 20;
+    h->budget = weight_budget ? weight_budget : (free_b > reserve ? free_b - reserve : 0);
+    h->name = std::string("HIP ") + prop.gcnArchName + (h->q8 ? " Q8 activations" : " FP32 accumulation");
+    const size_t colon = h->name.find(':');
+    if (colon != std::string::npos) h->name = h->name.substr(0, colon) + (h->q8 ? " Q8 activations" : " FP32 accumulation");
+    *out = h;
+    return EMPRISE_OK;
+}
+
+void emprise_hip_destroy(emprise_hip* h) {
+    if (!h) return;
+    (void)hipSetDevice(h->device);
+    (void)hipStreamSynchronize(h->stream);
+    for (auto& kv : h->graphs) (void)hipGraphExecDestroy(kv.second);
+    for (auto& kv : h->weights) (void)hipFree(kv.second.dev);
+    for (auto& kv : h->scratch) (void)hipFree(kv.second.ptr);
+    for (auto& ev : h->events) (void)hipEventDestroy(ev);
+    (void)hipStreamDestroy(h->stream);
+    delete h;
+}
+
+const char* emprise_hip_name(const emprise_hip* h) { return h ? h->name.c_str() : ""; }
+uint64_t emprise_hip_capacity(const emprise_hip* h) { return h ? h->budget : 0; }
+uint64_t emprise_hip_weight_bytes(const emprise_hip* h) { return h ? h->used : 0; }
+
+emprise_status emprise_hip_alloc(emprise_hip* h, size_t bytes, emprise_dev* out) {
+    if (!h || !out) return fail(EMPRISE_EINVAL, "null argument");
+    if (h->capturing) return fail(EMPRISE_ESTATE, "allocation during graph capture");
+    void* p = nullptr;
+    HIP_TRY(hipMalloc(&p, bytes ? bytes : 4));
+    *out = reinterpret_cast<emprise_dev>(p);
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_free(emprise_hip* h, emprise_dev buffer) {
+    if (!h) return fail(EMPRISE_EINVAL, "null backend");
+    if (!buffer) return EMPRISE_OK;
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    HIP_TRY(hipFree(reinterpret_cast<void*>(buffer)));
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_upload(emprise_hip* h, emprise_dev dst, const void* src, size_t bytes) {
+    if (!h || (!dst && bytes) || (!src && bytes)) return fail(EMPRISE_EINVAL, "null argument");
+    if (h->capturing) return fail(EMPRISE_ESTATE, "upload during graph capture");
+    HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), src, bytes, hipMemcpyHostToDevice, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_download(emprise_hip* h, void* dst, emprise_dev src, size_t bytes) {
+    if (!h || (!dst && bytes) || (!src && bytes)) return fail(EMPRISE_EINVAL, "null argument");
+    if (h->capturing) return fail(EMPRISE_ESTATE, "download during graph capture");
+    HIP_TRY(hipMemcpyAsync(dst, reinterpret_cast<const void*>(src), bytes, hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_fill(emprise_hip* h, emprise_dev dst, float value, size_t n) {
+    if (!h || (!dst && n)) return fail(EMPRISE_EINVAL, "null argument");
+    if (!n) return EMPRISE_OK;
+    return traced(h, "fill", n * 4, [&] { return launch_fill(reinterpret_cast<float*>(dst), value, n, h->stream); });
+}
+
+emprise_status emprise_hip_upload_weight(emprise_hip* h, uint32_t type, uint64_t cols, uint64_t rows, const void* data,
+                                         size_t len, emprise_weight* out) {
+    if (!h || !data || !out) return fail(EMPRISE_EINVAL, "null argument");
+    if (h->capturing) return fail(EMPRISE_ESTATE, "weight upload during graph capture");
+    if (!supported_type(type)) return fail(EMPRISE_EINVAL, "unsupported GGUF tensor encoding: %u", type);
+    if (!cols || !rows) return fail(EMPRISE_EINVAL, "zero tensor dimension");
+    if ((type == kQ6K || type == kQ4K) && cols % 256)
+        return fail(EMPRISE_EINVAL, "%s row must contain whole blocks", type == kQ6K ? "Q6_K" : "Q4_K");
+    if (rows > UINT64_MAX / cols) return fail(EMPRISE_EINVAL, "dimension overflow");
+    const uint64_t bytes = encoded_bytes(type, cols * rows);
+    if (!bytes || bytes != len) return fail(EMPRISE_EINVAL, "Incorrect encoded size: %zu for %llu x %llu", len,
+                                            (unsigned long long)rows, (unsigned long long)cols);
+    if (bytes > h->budget - std::min(h->budget, h->used))
+        return fail(EMPRISE_ENOMEM, "weight budget exceeded (%llu + %llu > %llu)", (unsigned long long)h->used,
+                    (unsigned long long)bytes, (unsigned long long)h->budget);
+    HIP_TRY(hipSetDevice(h->device));
+    Weight w;
+    w.type = type;
+    w.cols = cols;
+    w.rows = rows;
+    w.bytes = bytes;
+    HIP_TRY(hipMalloc(&w.dev, bytes));
+    const uint8_t* src = static_cast<const uint8_t*>(data);
+    hipError_t err = hipSuccess;
+    if (type == kQ6K || type == kQ4K) {
+        // re-lay out in slabs of rows through a host buffer
+        const uint64_t nb = cols / 256, row_bytes = nb * type_block_bytes(type);
+        const uint64_t slab_rows = std::max<uint64_t>(1, (64ull << 20) / row_bytes);
+        std::vector<uint8_t> buf((size_t)(std::min(rows, slab_rows) * row_bytes));
+        for (uint64_t r0 = 0; r0 < rows && err == hipSuccess; r0 += slab_rows) {
+            const uint64_t n = std::min(slab_rows, rows - r0);
+            parallel_rows(n, [&](uint64_t b, uint64_t e) {
+                for (uint64_t r = b; r < e; ++r) {
+                    const uint8_t* s = src + (r0 + r) * row_bytes;
+                    uint8_t* d = buf.data() + r * row_bytes;
+                    if (type == kQ6K) q6_row_to_device(s, d, nb);
+                    else q4_row_to_device(s, d, nb);
+                }
+            });
+            err = hipMemcpy(w.dev + r0 * row_bytes, buf.data(), (size_t)(n * row_bytes), hipMemcpyHostToDevice);
+        }
+    } else {
+        err = hipMemcpy(w.dev, src, bytes, hipMemcpyHostToDevice);
+    }
+    if (err != hipSuccess) {
+        (void)hipFree(w.dev);
+        return fail(EMPRISE_EDEVICE, "upload weights: %s", hipGetErrorString(err));
+    }
+    h->used += bytes;
+    const uint64_t id = h->next_weight++;
+    h->weights.emplace(id, w);
+    *out = id;
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_weight_free(emprise_hip* h, emprise_weight id) {
+    if (!h) return fail(EMPRISE_EINVAL, "null backend");
+    auto it = h->weights.find(id);
+    if (it == h->weights.end()) return fail(EMPRISE_EINVAL, "unknown weight handle");
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    HIP_TRY(hipFree(it->second.dev));
+    h->used -= it->second.bytes;
+    h->weights.erase(it);
+    return EMPRISE_OK;
+}
+
+emprise_dev emprise_hip_weight_data(const emprise_hip* h, emprise_weight id) {
+    const Weight* w = h ? h->weight(id) : nullptr;
+    return w ? reinterpret_cast<emprise_dev>(w->dev) : 0;
+}
+
+emprise_status emprise_hip_dequantize_rows(emprise_hip* h, emprise_weight id, uint64_t row0, uint64_t n, emprise_dev out) {
+    const Weight* w = h ? h->weight(id) : nullptr;
+    if (!w || !out) return fail(EMPRISE_EINVAL, "bad weight or output");
+    if (row0 > w->rows || n > w->rows - row0) return fail(EMPRISE_EINVAL, "rows out of range");
+    if (!n) return EMPRISE_OK;
+    return launched(launch_dequant_rows(w->dev, w->type, (int)w->cols, row0, n, reinterpret_cast<float*>(out), h->stream));
+}
+
+emprise_status emprise_hip_weight_download_gguf(emprise_hip* h, emprise_weight id, void* out, size_t len) {
+    const Weight* w = h ? h->weight(id) : nullptr;
+    if (!w || !out) return fail(EMPRISE_EINVAL, "bad weight or output");
+    if (len != w->bytes) return fail(EMPRISE_EINVAL, "length mismatch");
+    std::vector<uint8_t> buf(w->bytes);
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    HIP_TRY(hipMemcpy(buf.data(), w->dev, w->bytes, hipMemcpyDeviceToHost));
+    if (w->type == kQ6K || w->type == kQ4K) {
+        const uint64_t nb = w->cols / 256, row_bytes = nb * type_block_bytes(w->type);
+        auto* dst = static_cast<uint8_t*>(out);
+        parallel_rows(w->rows, [&](uint64_t b, uint64_t e) {
+            for (uint64_t r = b; r < e; ++r) {
+                if (w->type == kQ6K) q6_row_from_device(buf.data() + r * row_bytes, dst + r * row_bytes, nb);
+                else q4_row_from_device(buf.data() + r * row_bytes, dst + r * row_bytes, nb);
+            }
+        });
+    } else {
+        std::memcpy(out, buf.data(), w->bytes);
+    }
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_linear(emprise_hip* h, emprise_weight w, emprise_dev x, emprise_dev y) {
+    if (!h || !x || !y) return fail(EMPRISE_EINVAL, "null argument");
+    const Weight* wt;
+    TRY(check_weights(h, 1, &w, &wt));
+    Proj p{wt, reinterpret_cast<float*>(y)};
+    return run_matvec(h, &p, 1, kMvPlain, nullptr, reinterpret_cast<const float*>(x), nullptr, nullptr, 0, nullptr);
+}
+
+emprise_status emprise_hip_linear_many(emprise_hip* h, int n, const emprise_weight* w, emprise_dev x,
+                                       const emprise_dev* y) {
+    if (!h || !w || !x || !y || n < 1 || n > kMaxSeg) return fail(EMPRISE_EINVAL, "bad arguments");
+    const Weight* wt[kMaxSeg];
+    TRY(check_weights(h, n, w, wt));
+    Proj p[kMaxSeg];
+    for (int i = 0; i < n; ++i) p[i] = {wt[i], reinterpret_cast<float*>(y[i])};
+    return run_matvec(h, p, n, kMvPlain, nullptr, reinterpret_cast<const float*>(x), nullptr, nullptr, 0, nullptr);
+}
+
+emprise_status emprise_hip_linear_norm(emprise_hip* h, const emprise_hip_input* in, int n, const emprise_weight* w,
+                                       const emprise_dev* y) {
+    if (!h || !in || !in->x || !w || !y || n < 1 || n > kMaxSeg) return fail(EMPRISE_EINVAL, "bad arguments");
+    if (in->x_out && (in->x_out == in->x || in->x_out == in->delta)) return fail(EMPRISE_EINVAL, "x_out aliases an input");
+    const Weight* wt[kMaxSeg];
+    TRY(check_weights(h, n, w, wt));
+    Proj p[kMaxSeg];
+    for (int i = 0; i < n; ++i) p[i] = {wt[i], reinterpret_cast<float*>(y[i])};
+    return run_matvec(h, p, n, kMvPlain, in, nullptr, nullptr, nullptr, 0, nullptr);
+}
+
+emprise_status emprise_hip_linear_batch(emprise_hip* h, emprise_weight w, emprise_dev X, emprise_dev Y, int K) {
+    if (!h || !X || !Y || K < 1) return fail(EMPRISE_EINVAL, "bad arguments");
+    const Weight* wt;
+    TRY(check_weights(h, 1, &w, &wt));
+    for (int k = 0; k < K; ++k) {
+        Proj p{wt, reinterpret_cast<float*>(Y) + (size_t)k * wt->rows};
+        TRY(run_matvec(h, &p, 1, kMvPlain, nullptr, reinterpret_cast<const float*>(X) + (size_t)k * wt->cols, nullptr,
+                       nullptr, 0, nullptr));
+    }
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_ffn_gate_up(emprise_hip* h, const emprise_hip_input* in, emprise_dev x, emprise_weight gate,
+                                       emprise_weight up, emprise_dev hidden) {
+    if (!h || !hidden || (!in && !x)) return fail(EMPRISE_EINVAL, "bad arguments");
+    const Weight* g = h->weight(gate);
+    const Weight* u = h->weight(up);
+    if (!is_matrix(g) || !is_matrix(u) || g->rows != u->rows || g->cols != u->cols)
+        return fail(EMPRISE_EINVAL, "Feed-forward shape mismatch");
+    if (g->type == u->type) {
+        Proj p[2] = {{g, reinterpret_cast<float*>(hidden)}, {u, nullptr}};
+        return run_matvec(h, p, 2, kMvSwiglu, in, reinterpret_cast<const float*>(x), nullptr, nullptr, 0, nullptr);
+    }
+    void* ub;
+    TRY(h->get_scratch("ffn_up", g->rows * sizeof(float), &ub));
+    Proj p[2] = {{g, reinterpret_cast<float*>(hidden)}, {u, static_cast<float*>(ub)}};
+    TRY(run_matvec(h, p, 2, kMvPlain, in, reinterpret_cast<const float*>(x), nullptr, nullptr, 0, nullptr));
+    return traced(h, "swiglu", g->rows * 12, [&] { return launch_swiglu(reinterpret_cast<float*>(hidden), static_cast<float*>(ub), (int)g->rows, h->stream); });
+}
+
+emprise_status emprise_hip_feed_forward(emprise_hip* h, const emprise_hip_input* in, emprise_dev x, emprise_weight gate,
+                                        emprise_weight up, emprise_weight down, emprise_dev y) {
+    if (!h || !y) return fail(EMPRISE_EINVAL, "bad arguments");
+    const Weight* g = h->weight(gate);
+    const Weight* d = h->weight(down);
+    if (!is_matrix(g) || !is_matrix(d) || d->cols != g->rows) return fail(EMPRISE_EINVAL, "Feed-forward shape mismatch");
+    void* hb;
+    TRY(h->get_scratch("ffn_hidden", g->rows * sizeof(float), &hb));
+    TRY(emprise_hip_ffn_gate_up(h, in, x, gate, up, reinterpret_cast<emprise_dev>(hb)));
+    Proj p{d, reinterpret_cast<float*>(y)};
+    return run_matvec(h, &p, 1, kMvPlain, nullptr, static_cast<const float*>(hb), nullptr, nullptr, 0, nullptr);
+}
+
+emprise_status emprise_hip_rmsnorm(emprise_hip* h, emprise_dev x, emprise_weight w, emprise_dev out, int n, float eps) {
+    const Weight* wt = h ? h->weight(w) : nullptr;
+    if (!wt || !x || !out || n < 1) return fail(EMPRISE_EINVAL, "bad arguments");
+    if (wt->type != kF32 || wt->rows * wt->cols != (uint64_t)n) return fail(EMPRISE_EINVAL, "RMS normalization dimensions");
+    return traced(h, "rmsnorm", (uint64_t)n * 12, [&] { return launch_rmsnorm(reinterpret_cast<const float*>(x), reinterpret_cast<const float*>(wt->dev),
+                                   reinterpret_cast<float*>(out), n, eps, h->stream); });
+}
+
+emprise_status emprise_hip_add(emprise_hip* h, emprise_dev x, emprise_dev y, int n) {
+    if (!h || !x || !y || n < 0) return fail(EMPRISE_EINVAL, "bad arguments");
+    if (!n) return EMPRISE_OK;
+    return traced(h, "add", (uint64_t)n * 12, [&] { return launch_add(reinterpret_cast<float*>(x), reinterpret_cast<const float*>(y), n, h->stream); });
+}
+
+emprise_status emprise_hip_swiglu(emprise_hip* h, emprise_dev gate, emprise_dev up, int n) {
+    if (!h || !gate || !up || n < 0) return fail(EMPRISE_EINVAL, "bad arguments");
+    if (!n) return EMPRISE_OK;
+    return traced(h, "swiglu", (uint64_t)n * 12, [&] { return launch_swiglu(reinterpret_cast<float*>(gate), reinterpret_cast<const float*>(up), n, h->stream); });
+}
+
+emprise_status emprise_hip_embed(emprise_hip* h, emprise_weight embedding, emprise_dev token, emprise_dev out) {
+    const Weight* w = h ? h->weight(embedding) : nullptr;
+    if (!w || !token || !out) return fail(EMPRISE_EINVAL, "bad arguments");
+    return traced(h, "embed", w->bytes / w->rows + w->cols * 4, [&] { return launch_embed(w->dev, w->type, (int)w->cols, (int)w->rows, reinterpret_cast<const int*>(token),
+                                 reinterpret_cast<float*>(out), h->stream); });
+}
+
+emprise_status emprise_hip_argmax(emprise_hip* h, emprise_dev logits, int n, emprise_dev index) {
+    if (!h || !logits || !index || n < 1) return fail(EMPRISE_EINVAL, "bad arguments");
+    return traced(h, "argmax", (uint64_t)n * 4, [&] { return launch_argmax(reinterpret_cast<const float*>(logits), n, nullptr, reinterpret_cast<int*>(index), h->stream); });
+}
+
+emprise_status emprise_hip_quantize_q8(emprise_hip* h, emprise_dev x, int cols, emprise_dev q, emprise_dev scales) {
+    if (!h || !x || !q || !scales || cols < 32 || cols % 32) return fail(EMPRISE_EINVAL, "bad arguments");
+    return traced(h, "quantize_q8", (uint64_t)cols * 5, [&] { return launch_quantize_q8(reinterpret_cast<const float*>(x), cols, reinterpret_cast<int8_t*>(q),
+                                       reinterpret_cast<float*>(scales), h->stream); });
+}
+
+emprise_status emprise_hip_delta_net(emprise_hip* h, const emprise_hip_delta_net_params* p) {
+    if (!h || !p) return fail(EMPRISE_EINVAL, "null argument");
+    const int kd = p->key_heads * p->state_dim, vd = p->value_heads * p->state_dim, ch = 2 * kd + vd;
+    const Weight *conv = h->weight(p->conv), *a = h->weight(p->ssm_a), *dt = h->weight(p->dt), *nw = h->weight(p->norm);
+    if (p->key_heads < 1 || p->value_heads % p->key_heads || (p->state_dim != 64 && p->state_dim != 128) ||
+        p->conv_width < 1 || !conv || !a || !dt || !nw || conv->rows * conv->cols != (uint64_t)ch * p->conv_width ||
+        a->rows * a->cols != (uint64_t)p->value_heads || dt->rows * dt->cols != (uint64_t)p->value_heads ||
+        nw->rows * nw->cols != (uint64_t)p->state_dim || conv->type != kF32 || a->type != kF32 || dt->type != kF32 ||
+        nw->type != kF32)
+        return fail(EMPRISE_EINVAL, "Recurrent projection dimensions");
+    if (!p->qkv || !p->gate || !p->alpha || !p->beta || !p->conv_state || !p->rec_state || !p->out)
+        return fail(EMPRISE_EINVAL, "null buffer");
+    void* conv_out;
+    TRY(h->get_scratch("gdn_conv", (size_t)ch * sizeof(float), &conv_out));
+    TRY(traced(h, "delta_conv", (uint64_t)ch * (p->conv_width * 8 + 8), [&] { return launch_delta_conv(reinterpret_cast<const float*>(p->qkv), reinterpret_cast<const float*>(conv->dev),
+                                   reinterpret_cast<float*>(p->conv_state), static_cast<float*>(conv_out), ch,
+                                   p->conv_width, h->stream); }));
+    GdnArgs g{};
+    g.key_heads = p->key_heads;
+    g.value_heads = p->value_heads;
+    g.state_dim = p->state_dim;
+    g.conv_width = p->conv_width;
+    g.eps = p->eps;
+    g.qkv = static_cast<const float*>(conv_out);
+    g.gate = reinterpret_cast<const float*>(p->gate);
+    g.alpha = reinterpret_cast<const float*>(p->alpha);
+    g.beta = reinterpret_cast<const float*>(p->beta);
+    g.ssm_a = reinterpret_cast<const float*>(a->dev);
+    g.dt = reinterpret_cast<const float*>(dt->dev);
+    g.norm = reinterpret_cast<const float*>(nw->dev);
+    g.state = reinterpret_cast<float*>(p->rec_state);
+    g.out = reinterpret_cast<float*>(p->out);
+    return traced(h, "gdn_step", gdn_bytes(g), [&] { return launch_gdn(g, h->stream); });
+}
+
+emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent_params* p, const emprise_hip_input* in,
+                                     emprise_dev x, emprise_dev y) {
+    if (!h || !p || !y || (!in && !x)) return fail(EMPRISE_EINVAL, "null argument");
+    const int kd = p->key_heads * p->state_dim, vd = p->value_heads * p->state_dim, ch = 2 * kd + vd;
+    const emprise_weight ids[5] = {p->qkv_w, p->gate_w, p->alpha_w, p->beta_w, p->out_w};
+    const Weight* w[5];
+    TRY(check_weights(h, 5, ids, w));
+    const Weight *conv = h->weight(p->conv), *a = h->weight(p->ssm_a), *dt = h->weight(p->dt), *nw = h->weight(p->norm);
+    if (p->key_heads < 1 || p->value_heads % p->key_heads || (p->state_dim != 64 && p->state_dim != 128) ||
+        w[0]->rows != (uint64_t)ch || w[1]->rows != (uint64_t)vd || w[2]->rows != (uint64_t)p->value_heads ||
+        w[3]->rows != (uint64_t)p->value_heads || w[4]->cols != (uint64_t)vd || !conv || !a || !dt || !nw ||
+        conv->type != kF32 || a->type != kF32 || dt->type != kF32 || nw->type != kF32 ||
+        conv->rows * conv->cols != (uint64_t)ch * p->conv_width || a->rows * a->cols != (uint64_t)p->value_heads ||
+        dt->rows * dt->cols != (uint64_t)p->value_heads || nw->rows * nw->cols != (uint64_t)p->state_dim)
+        return fail(EMPRISE_EINVAL, "Recurrent projection dimensions");
+    if (!p->conv_state || !p->rec_state) return fail(EMPRISE_EINVAL, "null state buffer");
+    void* proj;
+    const size_t proj_n = (size_t)ch + vd + 2 * (size_t)p->value_heads + vd;
+    TRY(h->get_scratch("gdn_proj", proj_n * sizeof(float), &proj));
+    float* qkv = static_cast<float*>(proj);
+    float* gate = qkv + ch;
+    float* alpha = gate + vd;
+    float* beta = alpha + p->value_heads;
+    float* dn = beta + p->value_heads;
+    Proj pr[4] = {{w[0], qkv}, {w[1], gate}, {w[2], alpha}, {w[3], beta}};
+    // qkv first, so the conv1d + SiLU epilogue lands on its rows
+    TRY(run_matvec(h, pr, 4, kMvPlain, in, reinterpret_cast<const float*>(x), reinterpret_cast<const float*>(conv->dev),
+                   reinterpret_cast<float*>(p->conv_state), p->conv_width, nullptr));
+    GdnArgs g{};
+    g.key_heads = p->key_heads;
+    g.value_heads = p->value_heads;
+    g.state_dim = p->state_dim;
+    g.conv_width = p->conv_width;
+    g.eps = p->eps;
+    g.qkv = qkv;
+    g.gate = gate;
+    g.alpha = alpha;
+    g.beta = beta;
+    g.ssm_a = reinterpret_cast<const float*>(a->dev);
+    g.dt = reinterpret_cast<const float*>(dt->dev);
+    g.norm = reinterpret_cast<const float*>(nw->dev);
+    g.state = reinterpret_cast<float*>(p->rec_state);
+    g.out = dn;
+    TRY(traced(h, "gdn_step", gdn_bytes(g), [&] { return launch_gdn(g, h->stream); }));
+    Proj po{w[4], reinterpret_cast<float*>(y)};
+    return run_matvec(h, &po, 1, kMvPlain, nullptr, dn, nullptr, nullptr, 0, nullptr);
+}
+
+emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention_params* p, emprise_dev qkv,
+                                     emprise_dev out) {
+    if (!h || !p || !qkv || !out || !p->keys || !p->values || !p->position) return fail(EMPRISE_EINVAL, "null argument");
+    const Weight *qn = h->weight(p->q_norm), *kn = h->weight(p->k_norm);
+    if (p->heads < 1 || p->kv_heads < 1 || p->heads % p->kv_heads || p->heads / p->kv_heads > 8 ||
+        (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256) || p->rotary > p->head_dim || p->rotary % 2 ||
+        p->rotary < 0 || p->context < 1 || !qn || !kn || qn->type != kF32 || kn->type != kF32 ||
+        qn->rows * qn->cols != (uint64_t)p->head_dim || kn->rows * kn->cols != (uint64_t)p->head_dim)
+        return fail(EMPRISE_EINVAL, "Attention projection dimensions");
+    void* partial;
+    void* counter;
+    TRY(h->get_scratch("attn_partial", attention_partial_floats(p->heads, p->kv_heads, p->head_dim, p->context) * sizeof(float),
+                       &partial));
+    TRY(h->get_scratch("attn_counter", 64 * sizeof(unsigned), &counter, true));
+    if (p->kv_heads > 64) return fail(EMPRISE_EINVAL, "too many KV heads");
+    AttnArgs a{};
+    a.heads = p->heads;
+    a.kv_heads = p->kv_heads;
+    a.head_dim = p->head_dim;
+    a.rotary = p->rotary;
+    a.context = p->context;
+    a.eps = p->eps;
+    a.rope_base = p->rope_base;
+    a.q_norm = reinterpret_cast<const float*>(qn->dev);
+    a.k_norm = reinterpret_cast<const float*>(kn->dev);
+    a.qkv = reinterpret_cast<const float*>(qkv);
+    a.keys = reinterpret_cast<float*>(p->keys);
+    a.values = reinterpret_cast<float*>(p->values);
+    a.position = reinterpret_cast<const int*>(p->position);
+    a.out = reinterpret_cast<float*>(out);
+    a.partial = static_cast<float*>(partial);
+    a.counter = static_cast<unsigned*>(counter);
+    return traced(h, "attention", 0, [&] { return launch_attention(a, h->stream); });
+}
+
+emprise_status emprise_hip_reset_state(emprise_hip* h) {
+    if (!h) return fail(EMPRISE_EINVAL, "null backend");
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_sync(emprise_hip* h) {
+    if (!h) return fail(EMPRISE_EINVAL, "null backend");
+    if (h->capturing) return fail(EMPRISE_ESTATE, "sync during graph capture");
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_advance(emprise_hip* h, emprise_dev state, emprise_dev prompt, emprise_dev history,
+                                   emprise_dev next) {
+    if (!h || !state) return fail(EMPRISE_EINVAL, "null argument");
+    return traced(h, "advance", 16, [&] { return launch_advance(reinterpret_cast<int*>(state), reinterpret_cast<const int*>(prompt),
+                                   reinterpret_cast<int*>(history), reinterpret_cast<const int*>(next), h->stream); });
+}
+
+emprise_status emprise_hip_lm_head(emprise_hip* h, const emprise_hip_input* in, emprise_weight w, emprise_dev logits,
+                                   emprise_dev index) {
+    if (!h || !in || !in->x || !logits || !index) return fail(EMPRISE_EINVAL, "null argument");
+    if (in->x_out && (in->x_out == in->x || in->x_out == in->delta)) return fail(EMPRISE_EINVAL, "x_out aliases an input");
+    const Weight* wt;
+    TRY(check_weights(h, 1, &w, &wt));
+    void* key;
+    TRY(h->get_scratch("argmax_key", sizeof(unsigned long long), &key, true));
+    Proj p{wt, reinterpret_cast<float*>(logits)};
+    TRY(run_matvec(h, &p, 1, kMvArgmax, in, nullptr, nullptr, nullptr, 0, static_cast<unsigned long long*>(key)));
+    return traced(h, "argmax_finish", 16, [&] { return launch_argmax_finish(static_cast<unsigned long long*>(key), reinterpret_cast<int*>(index), h->stream); });
+}
+
+emprise_status emprise_hip_graph_begin(emprise_hip* h) {
+    if (!h) return fail(EMPRISE_EINVAL, "null backend");
+    if (h->capturing) return fail(EMPRISE_ESTATE, "already capturing");
+    HIP_TRY(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+    h->capturing = true;
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_graph_end(emprise_hip* h, emprise_graph* out) {
+    if (!h || !out) return fail(EMPRISE_EINVAL, "null argument");
+    if (!h->capturing) return fail(EMPRISE_ESTATE, "not capturing");
+    h->capturing = false;
+    hipGraph_t graph = nullptr;
+    HIP_TRY(hipStreamEndCapture(h->stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return fail(EMPRISE_EDEVICE, "graph instantiate: %s", hipGetErrorString(e));
+    const uint64_t id = h->next_graph++;
+    h->graphs.emplace(id, exec);
+    *out = id;
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_graph_launch(emprise_hip* h, emprise_graph g) {
+    if (!h) return fail(EMPRISE_EINVAL, "null backend");
+    auto it = h->graphs.find(g);
+    if (it == h->graphs.end()) return fail(EMPRISE_EINVAL, "unknown graph");
+    HIP_TRY(hipGraphLaunch(it->second, h->stream));
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_graph_destroy(emprise_hip* h, emprise_graph g) {
+    if (!h) return fail(EMPRISE_EINVAL, "null backend");
+    auto it = h->graphs.find(g);
+    if (it == h->graphs.end()) return fail(EMPRISE_EINVAL, "unknown graph");
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    HIP_TRY(hipGraphExecDestroy(it->second));
+    h->graphs.erase(it);
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_trace_begin(emprise_hip* h) {
+    if (!h) return fail(EMPRISE_EINVAL, "null backend");
+    if (h->capturing) return fail(EMPRISE_ESTATE, "trace during graph capture");
+    h->tracing = true;
+    h->trace.clear();
+    h->trace_used = 0;
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_trace_end(emprise_hip* h, emprise_hip_trace_record* out, size_t cap, size_t* n) {
+    if (!h || !n || (!out && cap)) return fail(EMPRISE_EINVAL, "null argument");
+    h->tracing = false;
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    size_t k = 0;
+    for (const auto& r : h->trace) {
+        if (k >= cap) break;
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, r.a, r.b));
+        out[k++] = {r.kernel, r.bytes, ms};
+    }
+    *n = k;
+    h->trace.clear();
+    h->trace_used = 0;
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_event_record(emprise_hip* h, int slot) {
+    if (!h || slot < 0 || slot >= 65536) return fail(EMPRISE_EINVAL, "bad event slot");
+    if (h->capturing) return fail(EMPRISE_ESTATE, "event during graph capture");
+    while ((int)h->events.size() <= slot) {
+        hipEvent_t ev;
+        HIP_TRY(hipEventCreate(&ev));
+        h->events.push_back(ev);
+    }
+    HIP_TRY(hipEventRecord(h->events[slot], h->stream));
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_hip_event_elapsed(emprise_hip* h, int start_slot, int end_slot, float* ms) {
+    if (!h || !ms || start_slot < 0 || start_slot >= (int)h->events.size() || end_slot < 0 ||
+        end_slot >= (int)h->events.size())
+        return fail(EMPRISE_EINVAL, "bad event slot");
+    HIP_TRY(hipEventSynchronize(h->events[end_slot]));
+    HIP_TRY(hipEventElapsedTime(ms, h->events[start_slot], h->events[end_slot]));
+    return EMPRISE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,130 @@
+// Gated DeltaNet decode step on gfx950 (Backend::delta_net, reference
+// backend.cpp:19-60; the CUDA delta_conv/delta_scan/delta_norm_gate, cuda.cpp:417-479).
+//
+// One workgroup per value head (8 waves). The head's q/k are L2-normalised inside the
+// workgroup (every wave redundantly; 2*state_dim values), the 64 KiB state of the head
+// is streamed once -- each wave loads all of its rows before any arithmetic so the
+// reads overlap -- updated in registers and written back, and the per-head RMSNorm x
+// SiLU(gate) is applied before the single write of the head's output. Lane l of a wave
+// holds state columns l, l+64 (state_dim = 64*E), so every row access is one coalesced
+// 256-byte (E=1) or 512-byte (E=2) transfer.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace emprise {
+namespace {
+
+constexpr int kGdnWaves = 8;
+
+__global__ void delta_conv_kernel(const float* qkv, const float* w, float* hist, float* out, int channels, int cw) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= channels) return;
+    float* h = hist + (size_t)c * cw;
+    const float* k = w + (size_t)c * cw;
+    float sum = 0.f;
+    for (int j = 0; j < cw - 1; ++j) {
+        const float hv = h[j + 1];
+        h[j] = hv;
+        sum += hv * k[j];
+    }
+    const float v = qkv[c];
+    h[cw - 1] = v;
+    sum += v * k[cw - 1];
+    out[c] = siluf_(sum);
+}
+
+template <int E>
+__global__ __launch_bounds__(kGdnWaves * 64) void gdn_kernel(GdnArgs a) {
+    constexpr int SD = 64 * E, RPW = SD / kGdnWaves;  // rows per wave
+    __shared__ float o_row[SD];
+    const int h = blockIdx.x, kh = h % a.key_heads;  // tiled V-head order (backend.cpp:37)
+    const int key_dim = a.key_heads * SD;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float* q = a.qkv + (size_t)kh * SD;
+    const float* k = a.qkv + key_dim + (size_t)kh * SD;
+    const float* v = a.qkv + 2 * (size_t)key_dim + (size_t)h * SD;
+    float* S = a.state + (size_t)h * SD * SD;
+
+    // issue the state reads of this wave's rows first
+    float s[RPW][E];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int e = 0; e < E; ++e) s[r][e] = S[(size_t)(wave * RPW + r) * SD + lane + 64 * e];
+
+    // q/k L2 normalisation (backend.cpp:30-35): qscale = 1/sqrt(sum q^2 + eps)/sqrt(SD)
+    float qv[E], kv[E], qs = 0.f, ks = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        qv[e] = q[lane + 64 * e];
+        kv[e] = k[lane + 64 * e];
+        qs += qv[e] * qv[e];
+        ks += kv[e] * kv[e];
+    }
+    qs = wave_sum(qs);
+    ks = wave_sum(ks);
+    const float qscale = 1.f / sqrtf(qs + a.eps) / sqrtf((float)SD), kscale = 1.f / sqrtf(ks + a.eps);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        qv[e] *= qscale;
+        kv[e] *= kscale;
+    }
+    const float decay = expf(a.ssm_a[h] * softplusf_(a.alpha[h] + a.dt[h]));
+    const float b = sigmoidf_(a.beta[h]);
+
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int d = wave * RPW + r;
+        float mem = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            s[r][e] *= decay;
+            mem += s[r][e] * kv[e];
+        }
+        mem = wave_sum(mem);
+        const float delta = (v[d] - mem) * b;
+        float sum = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            s[r][e] += kv[e] * delta;
+            sum += s[r][e] * qv[e];
+        }
+        sum = wave_sum(sum);
+#pragma unroll
+        for (int e = 0; e < E; ++e) S[(size_t)d * SD + lane + 64 * e] = s[r][e];
+        if (lane == 0) o_row[d] = sum;
+    }
+    __syncthreads();
+    // per-head RMSNorm with ssm_norm, then SiLU(gate) (backend.cpp:57-58)
+    if (wave == 0) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss += o_row[lane + 64 * e] * o_row[lane + 64 * e];
+        ss = wave_sum(ss);
+        const float scale = 1.f / sqrtf(ss / (float)SD + a.eps);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int j = lane + 64 * e;
+            a.out[(size_t)h * SD + j] = o_row[j] * (scale * a.norm[j]) * siluf_(a.gate[(size_t)h * SD + j]);
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_delta_conv(const float* qkv, const float* conv_w, float* conv_state, float* out, int channels,
+                             int conv_width, hipStream_t stream) {
+    hipLaunchKernelGGL(delta_conv_kernel, dim3((channels + 255) / 256), dim3(256), 0, stream, qkv, conv_w, conv_state,
+                       out, channels, conv_width);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream) {
+    const dim3 grid(a.value_heads), block(kGdnWaves * 64);
+    if (a.state_dim == 64) hipLaunchKernelGGL(gdn_kernel<1>, grid, block, 0, stream, a);
+    else if (a.state_dim == 128) hipLaunchKernelGGL(gdn_kernel<2>, grid, block, 0, stream, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace emprise

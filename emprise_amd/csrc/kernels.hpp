@@ -1,0 +1,97 @@
+// Host-side launch interface of the gfx950 kernels (internal to libemprise_hip.so).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace emprise {
+
+constexpr int kMaxSeg = 8;
+constexpr int kMvRows = 2;  // rows per wave iteration
+
+enum MvMode : int { kMvPlain = 0, kMvSwiglu = 1, kMvArgmax = 2 };
+
+// One projection of a grouped matvec launch.
+struct MvSeg {
+    const uint8_t* w;  // device layout of the weight
+    float* y;          // output (rows floats)
+    int rows;
+    int g0;  // first global row-group index of this segment
+};
+
+struct MvArgs {
+    MvSeg seg[kMaxSeg];
+    int nseg;
+    int groups;  // total row groups
+    int cols;
+    int mode;
+    // input transform: v = x + delta; x_out = v; input = rms(v) * norm
+    const float* x;
+    const float* delta;
+    float* x_out;
+    const float* norm;
+    float eps;
+    // kMvArgmax: running maximum key (value, -index), see argmax_key()
+    unsigned long long* argmax;
+    // causal conv1d + SiLU epilogue on segment 0 (the GDN qkv projection), or null
+    const float* conv_w;  // [rows][conv_width]
+    float* conv_state;    // [rows][conv_width]
+    int conv_width;
+};
+
+size_t matvec_lds_bytes(uint32_t type, int cols, bool q8);
+hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, hipStream_t stream);
+hipError_t launch_dequant_rows(const uint8_t* w, uint32_t type, int cols, uint64_t row0, uint64_t n, float* out,
+                               hipStream_t stream);
+
+// ---- Gated DeltaNet ----
+struct GdnArgs {
+    int key_heads, value_heads, state_dim, conv_width;
+    float eps;
+    const float* qkv;  // conv'd + SiLU'd channels (2*key_dim + value_dim)
+    const float* gate;
+    const float* alpha;
+    const float* beta;
+    const float* ssm_a;
+    const float* dt;
+    const float* norm;
+    float* state;  // [value_heads][state_dim][state_dim]
+    float* out;    // [value_dim]
+};
+// conv1d + SiLU over raw channels (delta_conv): out[c] = silu(conv(shifted history)).
+hipError_t launch_delta_conv(const float* qkv, const float* conv_w, float* conv_state, float* out, int channels,
+                             int conv_width, hipStream_t stream);
+hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream);
+
+// ---- attention ----
+struct AttnArgs {
+    int heads, kv_heads, head_dim, rotary, context;
+    float eps, rope_base;
+    const float* q_norm;
+    const float* k_norm;
+    const float* qkv;
+    float* keys;
+    float* values;
+    const int* position;
+    float* out;
+    float* partial;         // scratch: [kv_heads][chunks][group][head_dim + 2]
+    unsigned int* counter;  // scratch: [kv_heads], zero between launches
+};
+constexpr int kAttnChunk = 64;
+size_t attention_partial_floats(int heads, int kv_heads, int head_dim, int context);
+hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+
+// ---- small ops ----
+hipError_t launch_fill(float* dst, float value, size_t n, hipStream_t stream);
+hipError_t launch_fill_u64(unsigned long long* dst, unsigned long long value, size_t n, hipStream_t stream);
+hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t stream);
+hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream);
+hipError_t launch_swiglu(float* gate, const float* up, int n, hipStream_t stream);
+hipError_t launch_embed(const uint8_t* w, uint32_t type, int cols, int rows, const int* token, float* out,
+                        hipStream_t stream);
+hipError_t launch_argmax(const float* logits, int n, unsigned long long* key, int* index, hipStream_t stream);
+hipError_t launch_argmax_finish(const unsigned long long* key, int* index, hipStream_t stream);
+hipError_t launch_quantize_q8(const float* x, int cols, int8_t* q, float* scales, hipStream_t stream);
+hipError_t launch_advance(int* state, const int* prompt, int* history, const int* next, hipStream_t stream);
+
+}  // namespace emprise

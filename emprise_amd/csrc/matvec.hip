@@ -1,0 +1,390 @@
+// Dequant-matvec kernels for batch-1 decode on gfx950.
+//
+// One launch computes up to kMaxSeg projections that share one input vector
+// (Backend::linear / linear_many / the gate+up half of feed_forward,
+// reference cuda.cpp:199-304, 499-532, 567-596).
+//
+// Mapping: a workgroup of 4 waves stages the input vector once in LDS (with the
+// residual add + RMSNorm of the reference's dev_add/dev_rmsnorm fused in, and the
+// per-unit input sums the zero-point terms need), then each wave takes groups of R
+// rows. In a group, lane l handles units l, l+64, l+128, ... of every row, so one
+// vector load instruction covers 64 consecutive units: 768 contiguous bytes of Q6_K
+// codes, 1 KiB of Q4_K nibbles. Each lane keeps one FP32 accumulator per row; the 64
+// partials are summed with cross-lane shuffles at the end of the group.
+//
+// Arithmetic (FP32 path): weight = (d*sc)*(q-32) for Q6_K (quant.cpp:25-40) and
+// (d*sc)*q - dmin*m for Q4_K (quant.cpp:41-61). A unit's contribution is computed as
+// (d*sc) * (sum q*x - 32*sum x) and (d*sc)*(sum q*x) - (dmin*m)*(sum x): the same
+// products as the CPU path, grouped per unit. Only the order of FP32 additions
+// differs from the reference's sequential row sum.
+#include "common.hpp"
+#include "kernels.hpp"
+#include "decode.hpp"
+#include "layout.hpp"
+
+namespace emprise {
+
+namespace {
+
+template <int T> struct Fmt;
+template <> struct Fmt<kQ6K> { static constexpr int unit = 16, block = 210; };
+template <> struct Fmt<kQ4K> { static constexpr int unit = 32, block = 144; };
+
+// ---- input staging ------------------------------------------------------------------
+
+// xs[i] = rms(x + delta) * norm (or the plain input), usum[u] = sum of unit u of xs.
+__device__ void stage_input(const MvArgs& a, float* xs, float* usum, int unit, float* red) {
+    const int n = a.cols;
+    const bool writer = a.x_out && blockIdx.x == 0;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = a.x[i];
+        if (a.delta) v += a.delta[i];
+        if (writer) a.x_out[i] = v;
+        xs[i] = v;
+        ss += v * v;
+    }
+    if (a.norm) {
+        const float total = block_sum(ss, red);
+        const float scale = 1.f / sqrtf(total / (float)n + a.eps);
+        for (int i = threadIdx.x; i < n; i += blockDim.x) xs[i] = xs[i] * (scale * a.norm[i]);
+    }
+    __syncthreads();
+    const int units = n / unit;
+    for (int u = threadIdx.x; u < units; u += blockDim.x) {
+        float s = 0.f;
+        for (int i = 0; i < unit; ++i) s += xs[u * unit + i];
+        usum[u] = s;
+    }
+}
+
+// Q8 activations (quantize_x, cuda.cpp:547-559) computed in the prologue from the
+// staged FP32 input: per 32 values s = amax/127, q = round(v/s) with the unrounded s,
+// kept scale = fp16_rne(s). xq: n int8, xscale: n/32 floats, qsum: per 16-unit sum of q.
+__device__ void stage_q8(int n, const float* xs, int8_t* xq, float* xscale, int* qsum) {
+    for (int blk = threadIdx.x; blk < n / 32; blk += blockDim.x) {
+        float amax = 0.f;
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(xs[blk * 32 + i]));
+        const float s = amax / 127.f;
+        int s0 = 0, s1 = 0;
+        for (int i = 0; i < 32; ++i) {
+            const int q = s != 0.f ? (int)roundf(xs[blk * 32 + i] / s) : 0;
+            xq[blk * 32 + i] = (int8_t)q;
+            if (i < 16) s0 += q; else s1 += q;
+        }
+        xscale[blk] = half_bits_to_float(float_to_half_bits(s));
+        qsum[blk * 2] = s0;
+        qsum[blk * 2 + 1] = s1;
+    }
+}
+
+// ---- per-unit dot products --------------------------------------------------------
+
+__device__ __forceinline__ float dot4(uint32_t q, const float4& x, float acc) {
+    acc = fmaf(ubyte_f(q, 0), x.x, acc);
+    acc = fmaf(ubyte_f(q, 1), x.y, acc);
+    acc = fmaf(ubyte_f(q, 2), x.z, acc);
+    acc = fmaf(ubyte_f(q, 3), x.w, acc);
+    return acc;
+}
+
+// sum over the 16 codes of a Q6_K unit times x (codes 0..63, no zero point)
+__device__ __forceinline__ float q6_unit(uint32_t d0, uint32_t d1, uint32_t d2, const float4* x) {
+    const uint32_t a = d0 & 0x3F3F3F3Fu, b = d1 & 0x3F3F3F3Fu, c = d2 & 0x3F3F3F3Fu;
+    const uint32_t e = ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u);
+    float s0 = dot4(a, x[0], 0.f);
+    float s1 = dot4(b, x[1], 0.f);
+    s0 = dot4(c, x[2], s0);
+    s1 = dot4(e, x[3], s1);
+    return s0 + s1;
+}
+
+// sum over the 32 codes of a Q4_K unit times x
+__device__ __forceinline__ float q4_unit(const uint4& d, const float4* x) {
+    float s0 = dot4(d.x & 0x0F0F0F0Fu, x[0], 0.f);
+    float s1 = dot4(d.y & 0x0F0F0F0Fu, x[1], 0.f);
+    s0 = dot4(d.z & 0x0F0F0F0Fu, x[2], s0);
+    s1 = dot4(d.w & 0x0F0F0F0Fu, x[3], s1);
+    s0 = dot4((d.x >> 4) & 0x0F0F0F0Fu, x[4], s0);
+    s1 = dot4((d.y >> 4) & 0x0F0F0F0Fu, x[5], s1);
+    s0 = dot4((d.z >> 4) & 0x0F0F0F0Fu, x[6], s0);
+    s1 = dot4((d.w >> 4) & 0x0F0F0F0Fu, x[7], s1);
+    return s0 + s1;
+}
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// Contribution of unit u of one Q6_K row (FP32 activations).
+__device__ __forceinline__ float q6_row_unit(const uint8_t* row, int nb, int u, const float4* xv, float xsum) {
+    const uint8_t* q = row + (size_t)u * 12;
+    const uint32_t d0 = ld_u32(q), d1 = ld_u32(q + 4), d2 = ld_u32(q + 8);
+    const float sc = (float)(int8_t)row[(size_t)nb * 192 + u];
+    const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(row + (size_t)nb * 208 + 2 * (u >> 4)));
+    const float s = q6_unit(d0, d1, d2, xv);
+    return (d * sc) * fmaf(-32.f, xsum, s);
+}
+
+__device__ __forceinline__ float q4_row_unit(const uint8_t* row, int nb, int u, const float4* xv, float xsum) {
+    const uint4 d = *reinterpret_cast<const uint4*>(row + (size_t)u * 16);
+    const uint8_t* sp = row + (size_t)nb * 128 + (size_t)(u >> 3) * 12;
+    int sc, mn;
+    q4_scale_min(sp, u & 7, sc, mn);
+    const uint8_t* dp = row + (size_t)nb * 140 + (size_t)(u >> 3) * 4;
+    const float dd = half_bits_to_float(*reinterpret_cast<const uint16_t*>(dp));
+    const float dm = half_bits_to_float(*reinterpret_cast<const uint16_t*>(dp + 2));
+    const float s = q4_unit(d, xv);
+    return (dd * (float)sc) * s - (dm * (float)mn) * xsum;
+}
+
+// Q6_K unit with int8 activations (linear_q8, cuda.cpp:567-596): integer dot of the
+// codes with q8, minus 32*sum(q8), scaled by (d*sc) and the activation scale.
+__device__ __forceinline__ float q6_row_unit_q8(const uint8_t* row, int nb, int u, const int8_t* xq,
+                                                const float* xscale, const int* qsum) {
+    const uint8_t* q = row + (size_t)u * 12;
+    const uint32_t d0 = ld_u32(q), d1 = ld_u32(q + 4), d2 = ld_u32(q + 8);
+    const uint32_t a = d0 & 0x3F3F3F3Fu, b = d1 & 0x3F3F3F3Fu, c = d2 & 0x3F3F3F3Fu;
+    const uint32_t e = ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u);
+    const int* xv = reinterpret_cast<const int*>(xq + (size_t)u * 16);
+    int dot = __builtin_amdgcn_sdot4((int)a, xv[0], 0, false);
+    dot = __builtin_amdgcn_sdot4((int)b, xv[1], dot, false);
+    dot = __builtin_amdgcn_sdot4((int)c, xv[2], dot, false);
+    dot = __builtin_amdgcn_sdot4((int)e, xv[3], dot, false);
+    dot -= 32 * qsum[u];
+    const float sc = (float)(int8_t)row[(size_t)nb * 192 + u];
+    const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(row + (size_t)nb * 208 + 2 * (u >> 4)));
+    return ((float)dot * (d * sc)) * xscale[u >> 1];
+}
+
+// ---- the kernel -------------------------------------------------------------------
+
+// Causal conv1d step of channel c (backend.cpp:22-29): shift the history left, append
+// the new value, dot with the taps in history order, SiLU.
+__device__ __forceinline__ float conv_step(const float* w, float* hist, int cw, int c, float v) {
+    float* h = hist + (size_t)c * cw;
+    const float* k = w + (size_t)c * cw;
+    float sum = 0.f;
+    for (int j = 0; j < cw - 1; ++j) {
+        const float hv = h[j + 1];
+        h[j] = hv;
+        sum += hv * k[j];
+    }
+    h[cw - 1] = v;
+    sum += v * k[cw - 1];
+    return siluf_(sum);
+}
+
+// Orders floats as unsigned ints so that a larger key means a larger float; the low
+// word holds ~index so that equal values prefer the smaller index (std::max_element).
+__device__ __forceinline__ unsigned long long argmax_key(float v, int index) {
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)(~(uint32_t)index);
+}
+
+template <int T, int R, bool Q8, bool PAIR>
+__global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float red[16];
+    __shared__ unsigned long long block_best;
+    constexpr int UW = Fmt<T>::unit;
+    float* xs = reinterpret_cast<float*>(smem);
+    float* usum = xs + a.cols;
+    const int units = a.cols / UW;
+    int8_t* xq = reinterpret_cast<int8_t*>(usum + units);
+    float* xscale = reinterpret_cast<float*>(xq + a.cols);
+    int* qsum = reinterpret_cast<int*>(xscale + a.cols / 32);
+
+    stage_input(a, xs, usum, UW, red);
+    if constexpr (Q8) {
+        __syncthreads();
+        stage_q8(a.cols, xs, xq, xscale, qsum);
+    }
+    if (a.mode == kMvArgmax && threadIdx.x == 0) block_best = 0ull;
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = a.cols / 256;
+    const size_t row_bytes = (size_t)nb * Fmt<T>::block;
+    constexpr int NA = PAIR ? R * 2 : R;  // accumulators (pair mode: R gate + R up rows)
+    unsigned long long best = 0ull;
+
+    for (int g = blockIdx.x * 4 + wave; g < a.groups; g += gridDim.x * 4) {
+        int s = 0;
+        while (s + 1 < a.nseg && g >= a.seg[s + 1].g0) ++s;
+        const MvSeg seg = a.seg[s];
+        const int row0 = (g - seg.g0) * R;
+        const uint8_t* rp[NA];
+#pragma unroll
+        for (int r = 0; r < NA; ++r) {
+            const int rr = r < R ? row0 + r : row0 + r - R;
+            const int rc = rr < seg.rows ? rr : seg.rows - 1;
+            const uint8_t* base = r < R ? seg.w : a.seg[1].w;
+            rp[r] = base + (size_t)rc * row_bytes;
+        }
+        float acc[NA];
+#pragma unroll
+        for (int r = 0; r < NA; ++r) acc[r] = 0.f;
+
+        for (int u = lane; u < units; u += 64) {
+            if constexpr (Q8) {
+#pragma unroll
+                for (int r = 0; r < NA; ++r) acc[r] += q6_row_unit_q8(rp[r], nb, u, xq, xscale, qsum);
+            } else {
+                float4 xv[UW / 4];
+                const float4* xp = reinterpret_cast<const float4*>(xs + (size_t)u * UW);
+#pragma unroll
+                for (int i = 0; i < UW / 4; ++i) xv[i] = xp[i];
+                const float xsum = usum[u];
+#pragma unroll
+                for (int r = 0; r < NA; ++r) {
+                    if constexpr (T == kQ6K) acc[r] += q6_row_unit(rp[r], nb, u, xv, xsum);
+                    else acc[r] += q4_row_unit(rp[r], nb, u, xv, xsum);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NA; ++r) acc[r] = wave_sum(acc[r]);
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = row0 + r;
+                if (row < seg.rows) {
+                    if constexpr (PAIR) {
+                        seg.y[row] = siluf_(acc[r]) * acc[(R + r) % NA];
+                    } else if (a.conv_w && s == 0) {
+                        seg.y[row] = conv_step(a.conv_w, a.conv_state, a.conv_width, row, acc[r]);
+                    } else {
+                        seg.y[row] = acc[r];
+                        if (a.mode == kMvArgmax) {
+                            const unsigned long long k = argmax_key(acc[r], row);
+                            best = k > best ? k : best;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if (a.mode == kMvArgmax) {
+        if (lane == 0 && best) atomicMax(&block_best, best);
+        __syncthreads();
+        if (threadIdx.x == 0 && block_best) atomicMax(a.argmax, block_best);
+    }
+}
+
+// Plain-layout (F32 / F16 / BF16) matvec: one wave per row, lanes stride the columns.
+template <int T>
+__device__ __forceinline__ float raw_elem(const uint8_t* row, int k) {
+    if constexpr (T == kF32) return reinterpret_cast<const float*>(row)[k];
+    else if constexpr (T == kF16) return half_bits_to_float(reinterpret_cast<const uint16_t*>(row)[k]);
+    else return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(row)[k] << 16);
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void matvec_raw_kernel(MvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float red[16];
+    __shared__ unsigned long long block_best;
+    float* xs = reinterpret_cast<float*>(smem);
+    float* usum = xs + a.cols;
+    stage_input(a, xs, usum, 1 << 30, red);  // no unit sums needed
+    if (a.mode == kMvArgmax && threadIdx.x == 0) block_best = 0ull;
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t row_bytes = (size_t)a.cols * (T == kF32 ? 4 : 2);
+    const bool pair = a.mode == kMvSwiglu;
+    unsigned long long best = 0ull;
+    for (int g = blockIdx.x * 4 + wave; g < a.groups; g += gridDim.x * 4) {
+        int s = 0;
+        while (s + 1 < a.nseg && g >= a.seg[s + 1].g0) ++s;
+        const MvSeg seg = a.seg[s];
+        const int row = g - seg.g0;
+        const uint8_t* r0 = seg.w + (size_t)row * row_bytes;
+        const uint8_t* r1 = pair ? a.seg[1].w + (size_t)row * row_bytes : r0;
+        float acc0 = 0.f, acc1 = 0.f;
+        for (int k = lane; k < a.cols; k += 64) {
+            acc0 = fmaf(raw_elem<T>(r0, k), xs[k], acc0);
+            if (pair) acc1 = fmaf(raw_elem<T>(r1, k), xs[k], acc1);
+        }
+        acc0 = wave_sum(acc0);
+        if (pair) acc1 = wave_sum(acc1);
+        if (lane == 0) {
+            if (pair) seg.y[row] = siluf_(acc0) * acc1;
+            else {
+                seg.y[row] = acc0;
+                if (a.mode == kMvArgmax) {
+                    const unsigned long long k = argmax_key(acc0, row);
+                    best = k > best ? k : best;
+                }
+            }
+        }
+    }
+    if (a.mode == kMvArgmax) {
+        if (lane == 0 && best) atomicMax(&block_best, best);
+        __syncthreads();
+        if (threadIdx.x == 0 && block_best) atomicMax(a.argmax, block_best);
+    }
+}
+
+// ---- dequantisation of whole rows (dequantize(), quant.cpp:64-78) -------------------
+
+__global__ void dequant_rows_kernel(const uint8_t* w, uint32_t type, int cols, uint64_t row0, uint64_t n,
+                                    float* out) {
+    const uint64_t total = n * (uint64_t)cols;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = decode_element(w, type, cols, row0 + i / cols, (int)(i % cols));
+}
+
+}  // namespace
+
+// ---- host launchers ------------------------------------------------------------------
+
+size_t matvec_lds_bytes(uint32_t type, int cols, bool q8) {
+    if (type == kQ6K || type == kQ4K) {
+        const int unit = type == kQ6K ? 16 : 32;
+        size_t b = (size_t)cols * 4 + (size_t)(cols / unit) * 4;
+        if (q8) b += (size_t)cols + (size_t)(cols / 32) * 4 + (size_t)(cols / 16) * 4;
+        return b;
+    }
+    return (size_t)cols * 4 + 16;
+}
+
+hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, hipStream_t stream) {
+    const size_t lds = matvec_lds_bytes(type, a.cols, q8);
+    int blocks = (a.groups + 3) / 4;
+    if (blocks > grid_cap) blocks = grid_cap;
+    if (blocks < 1) blocks = 1;
+    const dim3 grid(blocks), block(256);
+    const bool pair = a.mode == kMvSwiglu;
+    switch (type) {
+    case kQ6K:
+        if (q8) {
+            if (pair) hipLaunchKernelGGL((matvec_kernel<kQ6K, kMvRows, true, true>), grid, block, lds, stream, a);
+            else hipLaunchKernelGGL((matvec_kernel<kQ6K, kMvRows, true, false>), grid, block, lds, stream, a);
+        } else {
+            if (pair) hipLaunchKernelGGL((matvec_kernel<kQ6K, kMvRows, false, true>), grid, block, lds, stream, a);
+            else hipLaunchKernelGGL((matvec_kernel<kQ6K, kMvRows, false, false>), grid, block, lds, stream, a);
+        }
+        break;
+    case kQ4K:
+        if (pair) hipLaunchKernelGGL((matvec_kernel<kQ4K, kMvRows, false, true>), grid, block, lds, stream, a);
+        else hipLaunchKernelGGL((matvec_kernel<kQ4K, kMvRows, false, false>), grid, block, lds, stream, a);
+        break;
+    case kF32: hipLaunchKernelGGL((matvec_raw_kernel<kF32>), grid, block, lds, stream, a); break;
+    case kF16: hipLaunchKernelGGL((matvec_raw_kernel<kF16>), grid, block, lds, stream, a); break;
+    case kBF16: hipLaunchKernelGGL((matvec_raw_kernel<kBF16>), grid, block, lds, stream, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_rows(const uint8_t* w, uint32_t type, int cols, uint64_t row0, uint64_t n, float* out,
+                               hipStream_t stream) {
+    const uint64_t total = n * (uint64_t)cols;
+    uint64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, w, type, cols, row0, n, out);
+    return hipGetLastError();
+}
+
+}  // namespace emprise

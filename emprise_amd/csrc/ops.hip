@@ -1,0 +1,152 @@
+// Small per-token kernels: fill, RMSNorm, residual add, SwiGLU, embedding row,
+// argmax, Q8 activation quantisation, position/token advance.
+#include "common.hpp"
+#include "decode.hpp"
+#include "kernels.hpp"
+
+namespace emprise {
+namespace {
+
+__global__ void fill_kernel(float* dst, float value, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = value;
+}
+
+__global__ void fill_u64_kernel(unsigned long long* dst, unsigned long long value, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = value;
+}
+
+// rmsnorm_kernel (cuda.cpp:533-542) / rms (model.cpp:19-25): out = x * (scale * w)
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const float* w, float* out, int n, float eps) {
+    __shared__ float red[16];
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
+    const float total = block_sum(ss, red);
+    const float scale = 1.f / sqrtf(total / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * (scale * w[i]);
+}
+
+__global__ void add_kernel(float* x, const float* y, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] += y[i];
+}
+
+// swiglu (cuda.cpp:560-566; backend.cpp:96-100): g * sigmoid(g) * u
+__global__ void swiglu_kernel(float* gate, const float* up, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) gate[i] = siluf_(gate[i]) * up[i];
+}
+
+__global__ void embed_kernel(const uint8_t* w, uint32_t type, int cols, int rows, const int* token, float* out) {
+    const int t = *token;
+    if (t < 0 || t >= rows) return;  // the host validates ids before they reach the device
+    for (int k = blockIdx.x * blockDim.x + threadIdx.x; k < cols; k += gridDim.x * blockDim.x)
+        out[k] = decode_element(w, type, cols, (uint64_t)t, k);
+}
+
+__device__ __forceinline__ unsigned long long order_key(float v, int index) {
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)(~(uint32_t)index);
+}
+
+// First maximum (std::max_element, model.cpp:499): one workgroup scans all logits.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n, int* index) {
+    __shared__ unsigned long long best;
+    if (threadIdx.x == 0) best = 0ull;
+    __syncthreads();
+    unsigned long long mine = 0ull;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const unsigned long long k = order_key(logits[i], i);
+        mine = k > mine ? k : mine;
+    }
+    atomicMax(&best, mine);
+    __syncthreads();
+    if (threadIdx.x == 0) *index = (int)~(uint32_t)(best & 0xffffffffull);
+}
+
+// Turns the key left by the LM-head epilogue into an index and clears the key for the
+// next token.
+__global__ void argmax_finish_kernel(unsigned long long* key, int* index) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        *index = (int)~(uint32_t)(*key & 0xffffffffull);
+        *key = 0ull;
+    }
+}
+
+// quantize_x (cuda.cpp:547-559): one 32-value block per thread.
+__global__ void quantize_q8_kernel(const float* x, int cols, int8_t* q, float* scales) {
+    const int blk = blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= cols / 32) return;
+    float amax = 0.f;
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[blk * 32 + i]));
+    const float s = amax / 127.f;
+    for (int i = 0; i < 32; ++i) q[blk * 32 + i] = (int8_t)(s != 0.f ? (int)roundf(x[blk * 32 + i] / s) : 0);
+    scales[blk] = half_bits_to_float(float_to_half_bits(s));
+}
+
+// state = {position, token, prompt_len}
+__global__ void advance_kernel(int* state, const int* prompt, int* history, const int* next) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        const int p = state[0];
+        const int nxt = next ? *next : 0;
+        if (history) history[p] = nxt;
+        state[0] = p + 1;
+        state[1] = (prompt && p + 1 < state[2]) ? prompt[p + 1] : nxt;
+    }
+}
+
+unsigned grid_for(size_t n, unsigned block, unsigned cap) {
+    size_t g = (n + block - 1) / block;
+    if (g > cap) g = cap;
+    return g ? (unsigned)g : 1u;
+}
+
+}  // namespace
+
+hipError_t launch_fill(float* dst, float value, size_t n, hipStream_t stream) {
+    hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n, 256, 4096)), dim3(256), 0, stream, dst, value, n);
+    return hipGetLastError();
+}
+hipError_t launch_fill_u64(unsigned long long* dst, unsigned long long value, size_t n, hipStream_t stream) {
+    hipLaunchKernelGGL(fill_u64_kernel, dim3(grid_for(n, 256, 4096)), dim3(256), 0, stream, dst, value, n);
+    return hipGetLastError();
+}
+hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t stream) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, stream, x, w, out, n, eps);
+    return hipGetLastError();
+}
+hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream) {
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for((size_t)n, 256, 1u << 20)), dim3(256), 0, stream, x, y, n);
+    return hipGetLastError();
+}
+hipError_t launch_swiglu(float* gate, const float* up, int n, hipStream_t stream) {
+    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for((size_t)n, 256, 1u << 20)), dim3(256), 0, stream, gate, up, n);
+    return hipGetLastError();
+}
+hipError_t launch_embed(const uint8_t* w, uint32_t type, int cols, int rows, const int* token, float* out,
+                        hipStream_t stream) {
+    hipLaunchKernelGGL(embed_kernel, dim3(grid_for((size_t)cols, 256, 64)), dim3(256), 0, stream, w, type, cols, rows,
+                       token, out);
+    return hipGetLastError();
+}
+hipError_t launch_argmax(const float* logits, int n, unsigned long long*, int* index, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, stream, logits, n, index);
+    return hipGetLastError();
+}
+hipError_t launch_argmax_finish(const unsigned long long* key, int* index, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(64), 0, stream, const_cast<unsigned long long*>(key), index);
+    return hipGetLastError();
+}
+hipError_t launch_quantize_q8(const float* x, int cols, int8_t* q, float* scales, hipStream_t stream) {
+    hipLaunchKernelGGL(quantize_q8_kernel, dim3(grid_for((size_t)cols / 32, 64, 1u << 20)), dim3(64), 0, stream, x,
+                       cols, q, scales);
+    return hipGetLastError();
+}
+hipError_t launch_advance(int* state, const int* prompt, int* history, const int* next, hipStream_t stream) {
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, state, prompt, history, next);
+    return hipGetLastError();
+}
+
+}  // namespace emprise

@@ -1,0 +1,160 @@
+// C ABI of the host library (include/emprise_host.h).
+#include <algorithm>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <stdexcept>
+#include <string>
+
+#include "emprise_host.h"
+#include "model.hpp"
+
+namespace emprise {
+void synth_write(const emprise_synth_config& c, const std::string& path);
+void synth_prompt(uint64_t seed, int vocab, size_t n, int* ids);
+}  // namespace emprise
+
+struct emprise_model {
+    std::unique_ptr<emprise::Model> model;
+    std::string name;
+};
+
+namespace {
+thread_local std::string g_error;
+
+template <class F> emprise_status guarded(F&& f) {
+    try {
+        f();
+        return EMPRISE_OK;
+    } catch (const std::invalid_argument& e) {
+        g_error = e.what();
+        return EMPRISE_EINVAL;
+    } catch (const std::out_of_range& e) {
+        g_error = e.what();
+        return EMPRISE_EINVAL;
+    } catch (const std::bad_alloc&) {
+        g_error = "out of host memory";
+        return EMPRISE_ENOMEM;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return EMPRISE_EDEVICE;
+    }
+}
+}  // namespace
+
+extern "C" {
+
+const char* emprise_host_last_error(void) { return g_error.c_str(); }
+
+emprise_status emprise_model_open(const emprise_model_options* o, emprise_model** out) {
+    if (!o || !o->path || !out) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    *out = nullptr;
+    return guarded([&] {
+        emprise::ModelOptions opt;
+        opt.path = o->path;
+        opt.context = o->context ? o->context : 4096;
+        opt.device = o->device;
+        opt.weight_vram_budget = o->weight_vram_budget;
+        opt.quantize_activations = o->quantize_activations != 0;
+        opt.fused = o->fused != 0;
+        opt.graph = o->graph != 0;
+        auto m = std::make_unique<emprise_model>();
+        m->model = std::make_unique<emprise::Model>(opt);
+        m->name = m->model->backend_name();
+        *out = m.release();
+    });
+}
+
+void emprise_model_close(emprise_model* m) { delete m; }
+
+const char* emprise_model_backend_name(const emprise_model* m) { return m ? m->name.c_str() : ""; }
+
+emprise_status emprise_model_get_info(const emprise_model* m, emprise_model_info* info) {
+    if (!m || !info) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    *info = m->model->info();
+    return EMPRISE_OK;
+}
+
+emprise_status emprise_model_reset(emprise_model* m) {
+    if (!m) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] { m->model->reset(); });
+}
+
+emprise_status emprise_model_evaluate(emprise_model* m, int token, float* logits) {
+    if (!m) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] {
+        auto v = m->model->evaluate(token, logits != nullptr);
+        if (logits) std::memcpy(logits, v.data(), v.size() * sizeof(float));
+    });
+}
+
+emprise_status emprise_model_last_hidden(emprise_model* m, float* hidden) {
+    if (!m || !hidden) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] {
+        auto v = m->model->last_hidden();
+        std::memcpy(hidden, v.data(), v.size() * sizeof(float));
+    });
+}
+
+emprise_status emprise_model_generate(emprise_model* m, const int* prompt, size_t prompt_len, size_t count, int* tokens,
+                                      size_t* emitted, double* arrivals) {
+    if (!m || (!prompt && prompt_len) || (!tokens && count) || !emitted) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] {
+        std::vector<double> arr;
+        auto out = m->model->generate(std::vector<int>(prompt, prompt + prompt_len), count, &arr);
+        std::memcpy(tokens, out.data(), out.size() * sizeof(int));
+        if (arrivals) std::memcpy(arrivals, arr.data(), arr.size() * sizeof(double));
+        *emitted = out.size();
+    });
+}
+
+emprise_status emprise_model_trace_step(emprise_model* m, int token, emprise_hip_trace_record* records, size_t cap,
+                                        size_t* n) {
+    if (!m || !n || (!records && cap)) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] {
+        auto rec = m->model->trace_step(token);
+        const size_t k = std::min(cap, rec.size());
+        std::memcpy(records, rec.data(), k * sizeof(emprise_hip_trace_record));
+        *n = k;
+    });
+}
+
+emprise_status emprise_synth_write(const emprise_synth_config* c, const char* path) {
+    if (!c || !path) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] { emprise::synth_write(*c, path); });
+}
+
+emprise_status emprise_synth_prompt(uint64_t seed, int vocab, size_t n, int* ids) {
+    if ((!ids && n) || vocab < 1) {
+        g_error = "bad argument";
+        return EMPRISE_EINVAL;
+    }
+    emprise::synth_prompt(seed, vocab, n, ids);
+    return EMPRISE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,391 @@
+// qwen35 decode graph (reference src/model.cpp) on the HIP backend.
+#include "model.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+
+namespace emprise {
+
+namespace {
+uint32_t type_id(WeightType t) { return static_cast<uint32_t>(t); }
+}  // namespace
+
+emprise_weight Model::upload(const std::string& name, uint64_t cols, uint64_t rows) {
+    const Tensor& t = gguf_->tensor(name);
+    if (t.shape.size() != 2 || t.shape[0] != cols || (rows && t.shape[1] != rows))
+        throw std::runtime_error("Expected matrix: " + name);
+    info_.weight_bytes += t.bytes;
+    return backend_->resident(type_id(t.type), t.shape[0], t.shape[1], gguf_->data(t), t.bytes);
+}
+
+// Small parameters (model.cpp:80-89) are decoded to FP32 on the host once, like the
+// reference's parameter cache, and kept on the device as F32 vectors.
+emprise_weight Model::upload_vector(const std::string& name, uint64_t n) {
+    const Tensor& t = gguf_->tensor(name);
+    if (t.elements != n) throw std::runtime_error("Parameter dimensions: " + name);
+    if (t.bytes > 16ull * 1024 * 1024) throw std::runtime_error("Unexpected non-matrix parameter size");
+    info_.weight_bytes += t.bytes;
+    std::vector<float> v(n);
+    const uint8_t* p = gguf_->data(t);
+    if (t.type == WeightType::f32) {
+        std::memcpy(v.data(), p, n * 4);
+    } else if (t.type == WeightType::f16 || t.type == WeightType::bf16) {
+        for (uint64_t i = 0; i < n; ++i) {
+            uint16_t b;
+            std::memcpy(&b, p + 2 * i, 2);
+            uint32_t u;
+            if (t.type == WeightType::bf16) {
+                u = uint32_t(b) << 16;
+            } else {
+                // exact fp16 -> fp32 (quant.cpp:8-17)
+                const uint32_t sign = uint32_t(b & 0x8000) << 16, ex = (b >> 10) & 31, frac = b & 1023;
+                if (ex == 0) {
+                    float f = std::ldexp(static_cast<float>(frac), -24);
+                    if (sign) f = -f;
+                    std::memcpy(&u, &f, 4);
+                } else {
+                    u = sign | (ex == 31 ? 0x7f800000u : (ex + 112) << 23) | (frac << 13);
+                }
+            }
+            std::memcpy(&v[i], &u, 4);
+        }
+    } else {
+        throw std::runtime_error("Unsupported parameter encoding: " + name);
+    }
+    return backend_->resident(EMPRISE_F32, n, 1, v.data(), n * 4);
+}
+
+Model::Model(const ModelOptions& options) : opt_(options) {
+    const auto start = std::chrono::steady_clock::now();
+    gguf_ = std::make_unique<Gguf>(opt_.path);
+    const Gguf& g = *gguf_;
+    const MetaValue* arch = g.meta("general.architecture");
+    if (!arch || arch->text != "qwen35") throw std::runtime_error("Only qwen35 is implemented");
+    auto integer = [&](const char* key) { return g.meta_int(std::string("qwen35.") + key); };
+    emprise_model_info& d = info_;
+    d.hidden = integer("embedding_length");
+    const MetaValue* nextn = g.meta("qwen35.nextn_predict_layers");
+    d.layers = integer("block_count") - (nextn ? static_cast<int>(nextn->number) : 0);
+    d.heads = integer("attention.head_count");
+    d.kv_heads = integer("attention.head_count_kv");
+    d.head_dim = integer("attention.key_length");
+    d.rotary = integer("rope.dimension_count");
+    d.key_heads = integer("ssm.group_count");
+    d.value_heads = integer("ssm.time_step_rank");
+    d.state_dim = integer("ssm.state_size");
+    d.conv_width = integer("ssm.conv_kernel");
+    d.eos = g.meta_int("tokenizer.ggml.eos_token_id");
+    d.eps = g.meta_float("qwen35.attention.layer_norm_rms_epsilon");
+    d.rope_base = g.meta_float("qwen35.rope.freq_base");
+    d.context = opt_.context;
+    // model.cpp:67-70
+    if (std::min({d.hidden, d.layers, d.heads, d.kv_heads, d.head_dim, d.rotary, d.key_heads, d.value_heads,
+                  d.state_dim, d.conv_width}) <= 0 ||
+        d.heads % d.kv_heads || d.value_heads % d.key_heads || d.rotary > d.head_dim || d.rotary % 2 ||
+        opt_.context == 0 || opt_.context > static_cast<size_t>(integer("context_length")))
+        throw std::runtime_error("Unsupported or invalid Qwen dimensions/context");
+
+    backend_ = std::make_unique<HipBackend>(opt_.device, opt_.weight_vram_budget, opt_.quantize_activations);
+    const uint64_t H = d.hidden;
+    const Tensor& emb = g.tensor("token_embd.weight");
+    if (emb.shape.size() != 2 || emb.shape[0] != H) throw std::runtime_error("token_embd shape");
+    d.vocab = static_cast<int>(emb.shape[1]);
+    embd_ = upload("token_embd.weight", H, 0);
+    output_ = upload("output.weight", H, static_cast<uint64_t>(d.vocab));  // required: no tied fallback (model.cpp:252)
+    output_norm_ = upload_vector("output_norm.weight", H);
+    const uint64_t kd = uint64_t(d.key_heads) * d.state_dim, vd = uint64_t(d.value_heads) * d.state_dim;
+    const uint64_t ch = 2 * kd + vd, qd = uint64_t(d.heads) * d.head_dim * 2, kvd = uint64_t(d.kv_heads) * d.head_dim;
+    uint64_t per_token = encoded_bytes(emb.type, H) + g.tensor("output.weight").bytes + g.tensor("output_norm.weight").bytes;
+    layers_.resize(static_cast<size_t>(d.layers));
+    for (int l = 0; l < d.layers; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        Layer& L = layers_[static_cast<size_t>(l)];
+        L.recurrent = g.has(p + "ssm_a");  // layer type from its tensors (model.cpp:75-78)
+        L.attn_norm = upload_vector(p + "attn_norm.weight", H);
+        L.post_norm = upload_vector(p + "post_attention_norm.weight", H);
+        const Tensor& fg = g.tensor(p + "ffn_gate.weight");
+        if (l == 0) d.ffn = static_cast<int>(fg.shape.at(1));
+        if (fg.shape.size() != 2 || static_cast<int>(fg.shape[1]) != d.ffn) throw std::runtime_error("FFN dimensions");
+        L.gate = upload(p + "ffn_gate.weight", H, d.ffn);
+        L.up = upload(p + "ffn_up.weight", H, d.ffn);
+        L.down = upload(p + "ffn_down.weight", d.ffn, H);
+        std::vector<std::string> names = {"attn_norm.weight", "post_attention_norm.weight", "ffn_gate.weight",
+                                          "ffn_up.weight", "ffn_down.weight"};
+        if (L.recurrent) {
+            L.qkv = upload(p + "attn_qkv.weight", H, ch);
+            L.zgate = upload(p + "attn_gate.weight", H, vd);
+            L.alpha = upload(p + "ssm_alpha.weight", H, d.value_heads);
+            L.beta = upload(p + "ssm_beta.weight", H, d.value_heads);
+            L.out = upload(p + "ssm_out.weight", vd, H);
+            L.conv = upload_vector(p + "ssm_conv1d.weight", ch * d.conv_width);
+            L.ssm_a = upload_vector(p + "ssm_a", d.value_heads);
+            L.dt = upload_vector(p + "ssm_dt.bias", d.value_heads);
+            L.ssm_norm = upload_vector(p + "ssm_norm.weight", d.state_dim);
+            L.conv_state = backend_->dev_alloc(ch * d.conv_width * 4);
+            L.rec_state = backend_->dev_alloc(vd * d.state_dim * 4);
+            names.insert(names.end(), {"attn_qkv.weight", "attn_gate.weight", "ssm_alpha.weight", "ssm_beta.weight",
+                                       "ssm_out.weight", "ssm_conv1d.weight", "ssm_a", "ssm_dt.bias", "ssm_norm.weight"});
+        } else {
+            L.q = upload(p + "attn_q.weight", H, qd);
+            L.k = upload(p + "attn_k.weight", H, kvd);
+            L.v = upload(p + "attn_v.weight", H, kvd);
+            L.o = upload(p + "attn_output.weight", uint64_t(d.heads) * d.head_dim, H);
+            L.q_norm = upload_vector(p + "attn_q_norm.weight", d.head_dim);
+            L.k_norm = upload_vector(p + "attn_k_norm.weight", d.head_dim);
+            L.keys = backend_->dev_alloc(opt_.context * kvd * 4);
+            L.values = backend_->dev_alloc(opt_.context * kvd * 4);
+            names.insert(names.end(), {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
+                                       "attn_q_norm.weight", "attn_k_norm.weight"});
+        }
+        for (const auto& n : names) per_token += g.tensor(p + n).bytes;
+    }
+    d.token_weight_bytes = per_token;
+    // activations
+    const uint64_t wide = std::max<uint64_t>({H, qd + 2 * kvd, uint64_t(d.heads) * d.head_dim, vd});
+    for (auto& x : x_) x = backend_->dev_alloc(H * 4);
+    delta_attn_ = backend_->dev_alloc(H * 4);
+    delta_ffn_ = backend_->dev_alloc(H * 4);
+    norm_ = backend_->dev_alloc(wide * 4);
+    tmp_ = backend_->dev_alloc(wide * 4);
+    qkv_ = backend_->dev_alloc((qd + 2 * kvd) * 4);
+    attn_out_ = backend_->dev_alloc(uint64_t(d.heads) * d.head_dim * 4);
+    logits_ = backend_->dev_alloc(uint64_t(d.vocab) * 4);
+    dev_state_ = backend_->dev_alloc(4 * sizeof(int));
+    dev_next_ = backend_->dev_alloc(sizeof(int));
+    dev_prompt_ = backend_->dev_alloc((opt_.context + 1) * sizeof(int));
+    dev_history_ = backend_->dev_alloc((opt_.context + 1) * sizeof(int));
+    reset();
+    // one eager step sizes every backend scratch buffer before any graph capture
+    set_state(0, 0, 0);
+    enqueue_step(true);
+    backend_->sync();
+    reset();
+    d.load_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
+}
+
+Model::~Model() = default;
+
+void Model::reset() {
+    for (const Layer& L : layers_) {
+        if (!L.recurrent) continue;
+        const uint64_t kd = uint64_t(info_.key_heads) * info_.state_dim, vd = uint64_t(info_.value_heads) * info_.state_dim;
+        backend_->dev_fill(L.conv_state, 0.f, (2 * kd + vd) * info_.conv_width);
+        backend_->dev_fill(L.rec_state, 0.f, vd * info_.state_dim);
+    }
+    position_ = 0;
+    set_state(0, 0, 0);
+}
+
+void Model::set_state(int position, int token, int prompt_len) {
+    const int s[4] = {position, token, prompt_len, 0};
+    backend_->dev_upload(dev_state_, s, sizeof s);
+}
+
+// One position. Token and position come from dev_state_ = {position, token,
+// prompt_len}; the last call advances them on the device.
+void Model::enqueue_step(bool logits) {
+    HipBackend& b = *backend_;
+    const emprise_model_info& d = info_;
+    const int H = d.hidden;
+    const emprise_dev pos = dev_state_, token = dev_state_ + sizeof(int);
+    const uint64_t qd = uint64_t(d.heads) * d.head_dim * 2, kvd = uint64_t(d.kv_heads) * d.head_dim;
+    auto recurrent_params = [&](const Layer& L) {
+        emprise_hip_recurrent_params p{};
+        p.qkv_w = L.qkv;
+        p.gate_w = L.zgate;
+        p.alpha_w = L.alpha;
+        p.beta_w = L.beta;
+        p.out_w = L.out;
+        p.conv = L.conv;
+        p.ssm_a = L.ssm_a;
+        p.dt = L.dt;
+        p.norm = L.ssm_norm;
+        p.key_heads = d.key_heads;
+        p.value_heads = d.value_heads;
+        p.state_dim = d.state_dim;
+        p.conv_width = d.conv_width;
+        p.eps = d.eps;
+        p.conv_state = L.conv_state;
+        p.rec_state = L.rec_state;
+        return p;
+    };
+    auto attention_params = [&](const Layer& L) {
+        emprise_hip_attention_params p{};
+        p.heads = d.heads;
+        p.kv_heads = d.kv_heads;
+        p.head_dim = d.head_dim;
+        p.rotary = d.rotary;
+        p.context = static_cast<int>(opt_.context);
+        p.eps = d.eps;
+        p.rope_base = d.rope_base;
+        p.q_norm = L.q_norm;
+        p.k_norm = L.k_norm;
+        p.keys = L.keys;
+        p.values = L.values;
+        p.position = pos;
+        return p;
+    };
+    const emprise_dev qkv_parts[3] = {qkv_, qkv_ + qd * 4, qkv_ + (qd + kvd) * 4};
+
+    b.dev_embed(embd_, token, x_[0]);
+    if (opt_.fused) {
+        // The residual adds and RMSNorms ride in the projections' prologues:
+        // x_next = x + delta; input = rms(x_next) * norm (model.cpp:217, :226-228, :243, :249).
+        int cur = 0;
+        emprise_dev pending = 0;
+        for (const Layer& L : layers_) {
+            emprise_hip_input in{x_[cur], pending, pending ? x_[cur ^ 1] : 0, L.attn_norm, d.eps};
+            if (pending) cur ^= 1;
+            if (L.recurrent) {
+                const auto p = recurrent_params(L);
+                b.dev_recurrent(p, &in, 0, delta_attn_);
+            } else {
+                const emprise_weight w[3] = {L.q, L.k, L.v};
+                b.dev_linear_norm(in, 3, w, qkv_parts);
+                b.dev_attention(attention_params(L), qkv_, attn_out_);
+                b.dev_linear(L.o, attn_out_, delta_attn_);
+            }
+            emprise_hip_input in2{x_[cur], delta_attn_, x_[cur ^ 1], L.post_norm, d.eps};
+            cur ^= 1;
+            b.dev_ffn(&in2, 0, L.gate, L.up, L.down, delta_ffn_);
+            pending = delta_ffn_;
+        }
+        if (logits) {
+            emprise_hip_input in{x_[cur], pending, x_[cur ^ 1], output_norm_, d.eps};
+            last_x_ = cur ^ 1;
+            hip_check(emprise_hip_lm_head(b.get(), &in, output_, logits_, dev_next_), "lm_head");
+        }
+    } else {
+        // One op per launch, in the order of evaluate_device (model.cpp:422-472).
+        const emprise_dev x = x_[0];
+        for (const Layer& L : layers_) {
+            b.dev_rmsnorm(x, L.attn_norm, norm_, H, d.eps);
+            if (L.recurrent) {
+                const auto p = recurrent_params(L);
+                b.dev_recurrent(p, nullptr, norm_, tmp_);
+            } else {
+                b.dev_linear(L.q, norm_, qkv_parts[0]);
+                b.dev_linear(L.k, norm_, qkv_parts[1]);
+                b.dev_linear(L.v, norm_, qkv_parts[2]);
+                b.dev_attention(attention_params(L), qkv_, attn_out_);
+                b.dev_linear(L.o, attn_out_, tmp_);
+            }
+            b.dev_add(x, tmp_, H);
+            b.dev_rmsnorm(x, L.post_norm, norm_, H, d.eps);
+            b.dev_ffn(nullptr, norm_, L.gate, L.up, L.down, tmp_);
+            b.dev_add(x, tmp_, H);
+        }
+        if (logits) {
+            last_x_ = 0;
+            b.dev_rmsnorm(x, output_norm_, norm_, H, d.eps);
+            b.dev_linear(output_, norm_, logits_);
+            b.dev_argmax(logits_, d.vocab, dev_next_);
+        }
+    }
+    hip_check(emprise_hip_advance(b.get(), dev_state_, dev_prompt_, logits ? dev_history_ : 0, logits ? dev_next_ : 0),
+              "advance");
+}
+
+emprise_graph Model::step_graph(bool logits) {
+    bool& have = logits ? have_graph_full_ : have_graph_prefill_;
+    emprise_graph& g = logits ? graph_full_ : graph_prefill_;
+    if (!have) {
+        backend_->graph_begin();
+        try {
+            enqueue_step(logits);
+        } catch (...) {
+            emprise_graph dead = 0;
+            (void)emprise_hip_graph_end(backend_->get(), &dead);
+            throw;
+        }
+        g = backend_->graph_end();
+        have = true;
+    }
+    return g;
+}
+
+std::vector<float> Model::evaluate(int token, bool want_logits) {
+    if (position_ >= opt_.context) throw std::runtime_error("Context budget exhausted");
+    if (token < 0 || token >= info_.vocab) throw std::out_of_range("Token ID");
+    set_state(static_cast<int>(position_), token, 0);
+    if (opt_.graph) backend_->graph_launch(step_graph(want_logits));
+    else enqueue_step(want_logits);
+    ++position_;
+    std::vector<float> out;
+    if (want_logits) {
+        out.resize(static_cast<size_t>(info_.vocab));
+        backend_->dev_download(out.data(), logits_, out.size() * 4);
+    } else {
+        backend_->sync();
+    }
+    return out;
+}
+
+std::vector<emprise_hip_trace_record> Model::trace_step(int token) {
+    if (position_ >= opt_.context) throw std::runtime_error("Context budget exhausted");
+    if (token < 0 || token >= info_.vocab) throw std::out_of_range("Token ID");
+    set_state(static_cast<int>(position_), token, 0);
+    backend_->sync();
+    hip_check(emprise_hip_trace_begin(backend_->get()), "trace_begin");
+    enqueue_step(true);
+    std::vector<emprise_hip_trace_record> rec(4096);
+    size_t n = 0;
+    hip_check(emprise_hip_trace_end(backend_->get(), rec.data(), rec.size(), &n), "trace_end");
+    rec.resize(n);
+    // attention reads K and V rows 0..position of its layer
+    const uint64_t kv = uint64_t(position_ + 1) * info_.kv_heads * info_.head_dim * 4 * 2;
+    for (auto& r : rec)
+        if (std::string(r.kernel) == "attention") r.bytes = kv;
+    ++position_;
+    return rec;
+}
+
+std::vector<float> Model::last_hidden() {
+    std::vector<float> h(static_cast<size_t>(info_.hidden));
+    backend_->dev_download(h.data(), x_[last_x_], h.size() * 4);
+    return h;
+}
+
+std::vector<int> Model::generate(const std::vector<int>& prompt, size_t count, std::vector<double>* arrivals) {
+    if (prompt.empty()) throw std::invalid_argument("Empty prompt");
+    if (prompt.size() > opt_.context || count > opt_.context - prompt.size())
+        throw std::invalid_argument("Prompt plus output exceeds context budget");
+    for (int t : prompt)
+        if (t < 0 || t >= info_.vocab) throw std::out_of_range("Token ID");
+    reset();
+    if (!count) return {};
+    const int n = static_cast<int>(prompt.size());
+    backend_->dev_upload(dev_prompt_, prompt.data(), prompt.size() * sizeof(int));
+    set_state(0, prompt[0], n);
+    backend_->event(0);
+    // prefill: every prompt position but the last skips the output head
+    for (int i = 0; i + 1 < n; ++i) {
+        if (opt_.graph) backend_->graph_launch(step_graph(false));
+        else enqueue_step(false);
+    }
+    // then count steps with the output head: the first one reads the last prompt
+    // token, each later one the previous greedy pick (model.cpp:497-502). The reference
+    // evaluates count-1 tokens after the prompt; the last launch here only produces
+    // the count-th pick.
+    for (size_t i = 0; i < count; ++i) {
+        if (opt_.graph) backend_->graph_launch(step_graph(true));
+        else enqueue_step(true);
+        backend_->event(static_cast<int>(1 + i));
+    }
+    backend_->sync();
+    std::vector<int> hist(count);
+    backend_->dev_download(hist.data(), dev_history_ + static_cast<uint64_t>(n - 1) * sizeof(int), count * sizeof(int));
+    std::vector<int> out;
+    for (size_t i = 0; i < count; ++i) {
+        if (hist[i] == info_.eos) break;  // model.cpp:500
+        out.push_back(hist[i]);
+        if (arrivals) arrivals->push_back(backend_->elapsed(0, static_cast<int>(1 + i)) * 1e-3);
+    }
+    position_ = static_cast<size_t>(n) + count;
+    return out;
+}
+
+}  // namespace emprise

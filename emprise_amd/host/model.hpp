@@ -1,0 +1,71 @@
+// qwen35 decode graph on the HIP backend: the reference's Model (include/emprise/
+// model.hpp:26-55, src/model.cpp) with its device path (evaluate_device,
+// model.cpp:422-472) extended so attention, the embedding row and the greedy pick also
+// stay on the device, and the whole step replays as one hipGraph.
+#pragma once
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "emprise_host.h"
+#include "gguf.hpp"
+#include "hip_backend.hpp"
+
+namespace emprise {
+
+struct ModelOptions {
+    std::string path;
+    size_t context = 4096;
+    int device = 0;
+    uint64_t weight_vram_budget = 0;
+    bool quantize_activations = false;
+    bool fused = true;
+    bool graph = true;
+};
+
+class Model {
+public:
+    explicit Model(const ModelOptions& options);
+    ~Model();
+    Model(const Model&) = delete;
+    Model& operator=(const Model&) = delete;
+
+    std::string backend_name() const { return backend_->name(); }
+    emprise_model_info info() const { return info_; }
+    void reset();
+    std::vector<float> evaluate(int token, bool want_logits = true);
+    std::vector<float> last_hidden();
+    std::vector<emprise_hip_trace_record> trace_step(int token);
+    // prefill + greedy loop; arrivals[i] = seconds from the first launch to token i
+    std::vector<int> generate(const std::vector<int>& prompt, size_t count, std::vector<double>* arrivals);
+
+private:
+    struct Layer {
+        bool recurrent = false;
+        emprise_weight attn_norm = 0, post_norm = 0, gate = 0, up = 0, down = 0;
+        emprise_weight qkv = 0, zgate = 0, alpha = 0, beta = 0, out = 0, conv = 0, ssm_a = 0, dt = 0, ssm_norm = 0;
+        emprise_weight q = 0, k = 0, v = 0, o = 0, q_norm = 0, k_norm = 0;
+        emprise_dev conv_state = 0, rec_state = 0, keys = 0, values = 0;
+    };
+    emprise_weight upload(const std::string& name, uint64_t cols, uint64_t rows);
+    emprise_weight upload_vector(const std::string& name, uint64_t n);
+    void enqueue_step(bool logits);  // one position, reading token/position from dev_state_
+    void set_state(int position, int token, int prompt_len);
+    emprise_graph step_graph(bool logits);
+
+    ModelOptions opt_;
+    std::unique_ptr<Gguf> gguf_;
+    std::unique_ptr<HipBackend> backend_;
+    emprise_model_info info_{};
+    std::vector<Layer> layers_;
+    emprise_weight embd_ = 0, output_ = 0, output_norm_ = 0;
+    emprise_dev x_[2] = {0, 0}, delta_attn_ = 0, delta_ffn_ = 0, norm_ = 0, tmp_ = 0, qkv_ = 0, attn_out_ = 0, logits_ = 0;
+    emprise_dev dev_state_ = 0, dev_next_ = 0, dev_prompt_ = 0, dev_history_ = 0;
+    int last_x_ = 0;  // residual buffer holding the stream after the last step
+    size_t position_ = 0;
+    emprise_graph graph_full_ = 0, graph_prefill_ = 0;
+    bool have_graph_full_ = false, have_graph_prefill_ = false;
+};
+
+}  // namespace emprise

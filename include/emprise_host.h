@@ -1,0 +1,102 @@
+/*
+ * emprise_host.h -- C ABI of the C++ host (libemprise_host.so): the GGUF loader,
+ * the qwen35 decode graph, the greedy loop and the --report numbers of the reference
+ * (v1.1 src/gguf.cpp, src/model.cpp, src/chat.cpp), running on the HIP backend of
+ * emprise_hip.h. Bindings (Python ctypes, the emprise-chat CLI) go through this header.
+ *
+ * Every call returns an emprise_status (emprise_hip.h); emprise_host_last_error()
+ * holds the message of the last failure on this thread.
+ */
+#ifndef EMPRISE_HOST_H
+#define EMPRISE_HOST_H
+#include <stddef.h>
+#include <stdint.h>
+
+#include "emprise_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+const char* emprise_host_last_error(void);
+
+/* ModelOptions (model.hpp:8-20) for the device path. */
+typedef struct {
+    const char* path;              /* GGUF file */
+    size_t context;                /* --context, default 4096 */
+    int device;                    /* HIP device ordinal */
+    uint64_t weight_vram_budget;   /* --vram-mib in bytes; 0 = free memory - 512 MiB */
+    int quantize_activations;      /* --fast-q8 */
+    int fused;                     /* 1: fused projection kernels (default); 0: one op per launch like
+                                      the reference's evaluate_device (model.cpp:422-472) */
+    int graph;                     /* 1: replay the decode step as a hipGraph (default) */
+} emprise_model_options;
+
+typedef struct emprise_model emprise_model;
+
+/* Model::Model (model.cpp:47-79, :474): parses the GGUF, checks the qwen35 dimensions,
+ * uploads every weight to the device. */
+emprise_status emprise_model_open(const emprise_model_options* options, emprise_model** out);
+void emprise_model_close(emprise_model* m);
+const char* emprise_model_backend_name(const emprise_model* m);
+
+typedef struct {
+    int hidden, layers, heads, kv_heads, head_dim, rotary;
+    int key_heads, value_heads, state_dim, conv_width, ffn, vocab, eos;
+    float eps, rope_base;
+    size_t context;
+    uint64_t weight_bytes;       /* GGUF bytes of every tensor uploaded */
+    uint64_t token_weight_bytes; /* GGUF bytes streamed per decoded token (matrices + one embedding row + vectors) */
+    double load_seconds;
+} emprise_model_info;
+emprise_status emprise_model_get_info(const emprise_model* m, emprise_model_info* info);
+
+/* Model::reset (model.cpp:479). */
+emprise_status emprise_model_reset(emprise_model* m);
+/* Model::evaluate (model.cpp:206-259) on the device: one position; logits (vocab
+ * floats) may be NULL. */
+emprise_status emprise_model_evaluate(emprise_model* m, int token, float* logits);
+/* The residual stream after the last evaluated position (Model::last_hidden_raw). */
+emprise_status emprise_model_last_hidden(emprise_model* m, float* hidden);
+
+/* Model::generate (model.cpp:488-503): prefill, then greedy tokens until count or EOS.
+ * tokens receives up to count ids, *emitted the number written, arrivals (optional,
+ * count doubles) the completion time of each token in seconds after the first
+ * prefill launch, measured with HIP events on the backend stream. */
+emprise_status emprise_model_generate(emprise_model* m, const int* prompt, size_t prompt_len, size_t count,
+                                      int* tokens, size_t* emitted, double* arrivals);
+
+/* One eager (non-graph) decode step at the current position with every kernel launch
+ * bracketed by HIP events (emprise_hip_trace_begin/end): per-launch kernel name,
+ * algorithmic bytes and milliseconds. Attention records carry the K/V bytes of the
+ * position they ran at. Advances the position like emprise_model_evaluate. */
+emprise_status emprise_model_trace_step(emprise_model* m, int token, emprise_hip_trace_record* records, size_t cap,
+                                        size_t* n);
+
+/* ---- synthetic qwen35 GGUF (test and benchmark inputs) ----------------------- */
+typedef struct {
+    uint64_t seed;
+    int hidden, layers, ffn, vocab;
+    int heads, kv_heads, head_dim, rotary;
+    int key_heads, value_heads, state_dim, conv_width;
+    int full_attention_interval; /* layer i is attention when (i+1) % interval == 0 */
+    int context_length;
+    float rope_base, eps;
+    int eos;
+    uint32_t matrix_type; /* EMPRISE_Q6_K or EMPRISE_Q4_K for every matrix */
+    int q4_k_m_mix;       /* 1: attn_v and ffn_down Q6_K, every other matrix Q4_K */
+} emprise_synth_config;
+
+/* Writes a GGUF v3 file with deterministic weights: counter-based SplitMix64 streams per
+ * tensor (so the bytes do not depend on thread count), normals by Irwin-Hall sums of
+ * twelve uniforms. Q6_K: codes uniform bytes, int8 sub-scales uniform in [-32, 31],
+ * d = fp16(|N|*2e-4). Q4_K: bytes uniform, d and dmin = fp16(|N|*1e-3). Norm weights
+ * 1 + N*0.02, ssm_a = -exp(0.5N - 2), ssm_dt.bias = 0.5N - 1, conv taps 0.5N. */
+emprise_status emprise_synth_write(const emprise_synth_config* config, const char* path);
+/* Seeded prompt ids uniform over [0, vocab). */
+emprise_status emprise_synth_prompt(uint64_t seed, int vocab, size_t n, int* ids);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,218 @@
+"""ctypes bindings of the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+liboracle.so is the plain-C restatement of the reference's CPU path (eo.c);
+_ref/libemprise_ref.so is the reference's own quant/gguf/backend sources compiled
+unchanged (present only where it was built from /root/reference). Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and
+only to check or time the CPU path -- never as the measured or shipped path.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_LIB = HERE / "liboracle.so"
+REF_LIB = HERE / "_ref" / "libemprise_ref.so"
+
+F32, F16, Q4_K, Q6_K, BF16 = 0, 1, 12, 14, 30
+
+_lib = None
+_ref = None
+_fp = ctypes.POINTER(ctypes.c_float)
+
+
+def _f(a: np.ndarray):
+    return a.ctypes.data_as(_fp)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not ORACLE_LIB.exists():
+            raise RuntimeError(f"{ORACLE_LIB} missing: run make -C oracle")
+        L = ctypes.CDLL(str(ORACLE_LIB))
+        vp, sz, u64, u32, i32, f32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_float
+        L.eo_half_to_float.restype = f32
+        L.eo_half_to_float.argtypes = [ctypes.c_uint16]
+        L.eo_encoded_bytes.restype = u64
+        L.eo_encoded_bytes.argtypes = [u32, u64]
+        L.eo_dequantize.restype = i32
+        L.eo_dequantize.argtypes = [u32, vp, sz, _fp, sz]
+        L.eo_matvec.restype = i32
+        L.eo_matvec.argtypes = [u32, vp, sz, _fp, sz, _fp, sz]
+        for fn in (L.eo_sigmoid, L.eo_silu, L.eo_softplus):
+            fn.restype = f32
+            fn.argtypes = [f32]
+        L.eo_rms.argtypes = [_fp, sz, _fp, f32]
+        L.eo_rope.argtypes = [_fp, i32, i32, f32]
+        L.eo_attention.argtypes = [i32, i32, i32, i32, f32, f32, _fp, _fp, _fp, _fp, _fp, _fp, _fp, sz, i32, _fp]
+        L.eo_delta_net.argtypes = [i32, i32, i32, i32, f32] + [_fp] * 11
+        L.eo_feed_forward.restype = i32
+        L.eo_feed_forward.argtypes = [u32, vp, u32, vp, u32, vp, sz, sz, _fp, _fp]
+        L.eo_model_load.restype = vp
+        L.eo_model_load.argtypes = [ctypes.c_char_p, sz, i32, ctypes.c_char_p, sz]
+        L.eo_model_free.argtypes = [vp]
+        L.eo_model_vocab.restype = i32
+        L.eo_model_vocab.argtypes = [vp]
+        L.eo_model_hidden.restype = i32
+        L.eo_model_hidden.argtypes = [vp]
+        L.eo_model_reset.argtypes = [vp]
+        L.eo_model_evaluate.restype = i32
+        L.eo_model_evaluate.argtypes = [vp, i32, _fp]
+        L.eo_model_generate.restype = i32
+        L.eo_model_generate.argtypes = [vp, ctypes.POINTER(ctypes.c_int), sz, sz, ctypes.POINTER(ctypes.c_int), _fp]
+        L.eo_model_last_hidden.restype = i32
+        L.eo_model_last_hidden.argtypes = [vp, _fp]
+        L.eo_last_error.restype = ctypes.c_char_p
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return REF_LIB.exists()
+
+
+def ref() -> ctypes.CDLL:
+    global _ref
+    if _ref is None:
+        if not REF_LIB.exists():
+            raise RuntimeError(f"{REF_LIB} missing (built only where the reference tree is mounted)")
+        R = ctypes.CDLL(str(REF_LIB))
+        vp, sz, u64, u32, i32, f32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_float
+        R.ref_last_error.restype = ctypes.c_char_p
+        R.ref_half_to_float.restype = f32
+        R.ref_half_to_float.argtypes = [ctypes.c_uint16]
+        R.ref_encoded_bytes.restype = i32
+        R.ref_encoded_bytes.argtypes = [u32, u64, ctypes.POINTER(u64)]
+        R.ref_dequantize.restype = i32
+        R.ref_dequantize.argtypes = [u32, vp, sz, _fp, sz]
+        R.ref_matvec.restype = i32
+        R.ref_matvec.argtypes = [u32, vp, sz, _fp, sz, _fp, sz]
+        R.ref_open.restype = vp
+        R.ref_open.argtypes = [ctypes.c_char_p, u64]
+        R.ref_close.argtypes = [vp]
+        R.ref_tensor_info.restype = i32
+        R.ref_tensor_info.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(u32), ctypes.POINTER(u64), ctypes.POINTER(u32), ctypes.POINTER(u64)]
+        R.ref_tensor_read.restype = i32
+        R.ref_tensor_read.argtypes = [vp, ctypes.c_char_p, vp, u64]
+        R.ref_metadata_json.restype = i32
+        R.ref_metadata_json.argtypes = [vp, ctypes.c_char_p, sz]
+        R.ref_linear.restype = i32
+        R.ref_linear.argtypes = [vp, ctypes.c_char_p, _fp, sz, _fp, sz]
+        R.ref_feed_forward.restype = i32
+        R.ref_feed_forward.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _fp, sz, _fp]
+        R.ref_delta_net.restype = i32
+        R.ref_delta_net.argtypes = [vp, i32, i32, i32, i32, f32] + [_fp] * 11
+        R.ref_recurrent_block.restype = i32
+        R.ref_recurrent_block.argtypes = [vp, ctypes.c_char_p, i32, i32, i32, i32, f32, _fp, _fp, _fp, _fp, _fp, sz, _fp, _fp, _fp]
+        _ref = R
+    return _ref
+
+
+# ---- numpy-facing helpers -------------------------------------------------------
+
+def half_to_float(h: int) -> float:
+    return lib().eo_half_to_float(h)
+
+
+def dequantize(wtype: int, raw: bytes, n: int) -> np.ndarray:
+    buf = np.frombuffer(raw, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    if lib().eo_dequantize(wtype, buf.ctypes.data, buf.nbytes, _f(out), n):
+        raise ValueError(lib().eo_last_error().decode())
+    return out
+
+
+def matvec(wtype: int, raw, x: np.ndarray, rows: int) -> np.ndarray:
+    buf = np.frombuffer(memoryview(raw).cast("B"), dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    if lib().eo_matvec(wtype, buf.ctypes.data, buf.nbytes, _f(x), x.size, _f(y), rows):
+        raise ValueError(lib().eo_last_error().decode())
+    return y
+
+
+def rms(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    y = np.array(x, dtype=np.float32, copy=True)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    lib().eo_rms(_f(y), y.size, _f(w), eps)
+    return y
+
+
+def rope(x: np.ndarray, rotary: int, pos: int, base: float) -> np.ndarray:
+    y = np.array(x, dtype=np.float32, copy=True)
+    lib().eo_rope(_f(y), rotary, pos, base)
+    return y
+
+
+def delta_net(key_heads, value_heads, state_dim, conv_width, eps, qkv, gate, alpha, beta, conv, ssm_a, dt, norm,
+              conv_state, rec_state):
+    """Backend::delta_net restated; conv_state/rec_state are updated in place."""
+    vd = value_heads * state_dim
+    out = np.empty(vd, dtype=np.float32)
+    args = [np.ascontiguousarray(a, dtype=np.float32) for a in (qkv, gate, alpha, beta, conv, ssm_a, dt, norm)]
+    lib().eo_delta_net(key_heads, value_heads, state_dim, conv_width, eps, *[_f(a) for a in args],
+                       _f(conv_state), _f(rec_state), _f(out))
+    return out
+
+
+def attention(heads, kv_heads, head_dim, rotary, rope_base, eps, q_norm, k_norm, qg, k, v, keys, values, length, pos):
+    """attention_preout restated; keys/values (context x kv*hd) get row length-1."""
+    out = np.empty(heads * head_dim, dtype=np.float32)
+    qg = np.array(qg, dtype=np.float32, copy=True)
+    k = np.array(k, dtype=np.float32, copy=True)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    qn = np.ascontiguousarray(q_norm, dtype=np.float32)
+    kn = np.ascontiguousarray(k_norm, dtype=np.float32)
+    lib().eo_attention(heads, kv_heads, head_dim, rotary, rope_base, eps, _f(qn), _f(kn), _f(qg), _f(k), _f(v),
+                       _f(keys), _f(values), length, pos, _f(out))
+    return out
+
+
+class Model:
+    """The whole CPU decode path over a GGUF file (Model::Impl::evaluate restated)."""
+
+    def __init__(self, path: str, context: int = 4096, threads: int = 0):
+        err = ctypes.create_string_buffer(512)
+        self.m = lib().eo_model_load(str(path).encode(), context, threads, err, 512)
+        if not self.m:
+            raise RuntimeError(err.value.decode())
+        self.vocab = lib().eo_model_vocab(self.m)
+        self.hidden = lib().eo_model_hidden(self.m)
+
+    def close(self):
+        if self.m:
+            lib().eo_model_free(self.m)
+            self.m = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        lib().eo_model_reset(self.m)
+
+    def evaluate(self, token: int, logits: bool = True):
+        out = np.empty(self.vocab, dtype=np.float32) if logits else None
+        if lib().eo_model_evaluate(self.m, token, _f(out) if logits else None):
+            raise RuntimeError(lib().eo_last_error().decode())
+        return out
+
+    def last_hidden(self) -> np.ndarray:
+        out = np.empty(self.hidden, dtype=np.float32)
+        lib().eo_model_last_hidden(self.m, _f(out))
+        return out
+
+    def generate(self, prompt, count: int):
+        p = (ctypes.c_int * len(prompt))(*prompt)
+        toks = (ctypes.c_int * max(count, 1))()
+        margins = np.empty(max(count, 1), dtype=np.float32)
+        n = lib().eo_model_generate(self.m, p, len(prompt), count, toks, _f(margins))
+        if n < 0:
+            raise RuntimeError(lib().eo_last_error().decode())
+        return list(toks[:n]), margins[:n].copy()

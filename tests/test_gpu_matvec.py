@@ -1,0 +1,219 @@
+"""Dequant-matvec parity on the GPU through the C ABI against the CPU oracle.
+
+Bars (north star): dequantised weights bit-exact; FP32 outputs within max-abs error
+1e-4 * max|ref|; the Q8 path within 1e-3 + 1e-4*|ref| of the CPU matvec on the
+explicitly quantised input (reference tests/core.cpp:115, :119-129).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from emprise_amd import BF16, F16, F32, Q4_K, Q6_K, Input, InvalidArgument
+from synth import matrix
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _close(got, ref, tol=TOL):
+    err = np.max(np.abs(got.astype(np.float64) - ref.astype(np.float64)))
+    bound = tol * max(np.max(np.abs(ref)), 1e-30)
+    assert err <= bound, f"max abs err {err:.3e} > {bound:.3e}"
+
+
+def _run_linear(be, wtype, rows, cols, seed, x=None):
+    rng = np.random.default_rng(seed)
+    raw = matrix(rng, wtype, rows, cols)
+    if x is None:
+        x = rng.standard_normal(cols).astype(np.float32)
+    w = be.upload_weight(wtype, cols, rows, raw)
+    xd, yd = be.to_device(x), be.alloc(rows * 4)
+    be.linear(w, xd, yd)
+    y = be.download(yd, rows)
+    be.free(xd)
+    be.free(yd)
+    be.weight_free(w)
+    return raw, x, y
+
+
+@pytest.mark.parametrize("wtype", [Q6_K, Q4_K, F32, F16, BF16])
+@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 512), (64, 1536), (129, 4096), (33, 12288)])
+def test_linear_small_vs_oracle(backend, wtype, rows, cols):
+    raw, x, y = _run_linear(backend, wtype, rows, cols, seed=rows * 7 + cols + wtype)
+    _close(y, oracle.matvec(wtype, raw, x, rows))
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (12288, 4096), (4096, 12288)])
+@pytest.mark.parametrize("wtype", [Q6_K, Q4_K])
+def test_linear_config1_shapes(backend, wtype, rows, cols):
+    raw, x, y = _run_linear(backend, wtype, rows, cols, seed=rows + cols + wtype)
+    _close(y, oracle.matvec(wtype, raw, x, rows))
+
+
+@pytest.mark.parametrize("wtype", [Q6_K, Q4_K])
+def test_linear_lm_head(backend, wtype):
+    rows, cols = 151936, 4096
+    raw, x, y = _run_linear(backend, wtype, rows, cols, seed=5 + wtype)
+    row_bytes = len(raw) // rows
+    # oracle on three row windows: first, middle, last (rows are independent)
+    for r0 in (0, rows // 2 - 700, rows - 1500):
+        n = 1500
+        ref = oracle.matvec(wtype, raw[r0 * row_bytes:(r0 + n) * row_bytes], x, n)
+        _close(y[r0:r0 + n], ref)
+    assert np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("wtype,rows,cols", [(Q6_K, 300, 4096), (Q4_K, 300, 4096), (Q6_K, 5, 1536), (Q4_K, 7, 512),
+                                             (F16, 9, 512), (BF16, 9, 512), (F32, 9, 256)])
+def test_dequantize_bit_exact(backend, wtype, rows, cols):
+    rng = np.random.default_rng(11)
+    raw = matrix(rng, wtype, rows, cols)
+    w = backend.upload_weight(wtype, cols, rows, raw)
+    out = backend.alloc(rows * cols * 4)
+    backend.dequantize_rows(w, 0, rows, out)
+    got = backend.download(out, rows * cols)
+    ref = oracle.dequantize(wtype, raw, rows * cols)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # the device re-layout is lossless: reading it back restores the GGUF bytes
+    assert backend.weight_download_gguf(w, len(raw)) == raw
+    backend.free(out)
+    backend.weight_free(w)
+
+
+def test_q6k_subnormal_and_extreme_scales(backend):
+    """fp16 d subnormal/largest and sc at -32/31 keep exact products (no flush)."""
+    rng = np.random.default_rng(3)
+    from synth import q6k_blocks
+    b = q6k_blocks(rng, 64)
+    d_bits = np.array([0x0001, 0x03ff, 0x0400, 0x7bff, 0x3c00, 0x8001, 0x0200, 0x0010] * 8, dtype=np.uint16)
+    b[:, 208:210] = d_bits.view(np.uint8).reshape(64, 2)
+    b[::2, 192:208] = np.int8(-32).view(np.uint8)
+    b[1::2, 192:208] = np.int8(31).view(np.uint8)
+    raw = b.tobytes()
+    rows, cols = 4, 4096
+    w = backend.upload_weight(Q6_K, cols, rows, raw)
+    out = backend.alloc(rows * cols * 4)
+    backend.dequantize_rows(w, 0, rows, out)
+    got = backend.download(out, rows * cols)
+    ref = oracle.dequantize(Q6_K, raw, rows * cols)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    backend.free(out)
+    backend.weight_free(w)
+
+
+def test_linear_many_matches_single(backend):
+    rng = np.random.default_rng(21)
+    cols = 4096
+    shapes = [8192, 4096, 32, 32]  # GDN qkv, gate, alpha, beta
+    raws = [matrix(rng, Q6_K, r, cols) for r in shapes]
+    x = rng.standard_normal(cols).astype(np.float32)
+    ws = [backend.upload_weight(Q6_K, cols, r, raw) for r, raw in zip(shapes, raws)]
+    xd = backend.to_device(x)
+    ys = [backend.alloc(r * 4) for r in shapes]
+    backend.linear_many(ws, xd, ys)
+    many = [backend.download(y, r) for y, r in zip(ys, shapes)]
+    for w, y, r, got in zip(ws, ys, shapes, many):
+        backend.linear(w, xd, y)
+        assert np.array_equal(backend.download(y, r), got)
+    for raw, r, got in zip(raws, shapes, many):
+        _close(got, oracle.matvec(Q6_K, raw, x, r))
+
+
+def test_linear_norm_fuses_add_and_rmsnorm(backend):
+    rng = np.random.default_rng(22)
+    cols, rows, eps = 4096, 1024, 1e-6
+    raw = matrix(rng, Q6_K, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    delta = rng.standard_normal(cols).astype(np.float32)
+    nw = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
+    w = backend.upload_weight(Q6_K, cols, rows, raw)
+    nwd = backend.vector(nw)
+    xd, dd, xo, yd = backend.to_device(x), backend.to_device(delta), backend.alloc(cols * 4), backend.alloc(rows * 4)
+    backend.linear_norm(Input(xd, dd, xo, nwd, eps), [w], [yd])
+    v = x + delta
+    assert np.array_equal(backend.download(xo, cols), v)
+    ref = oracle.matvec(Q6_K, raw, oracle.rms(v, nw, eps), rows)
+    _close(backend.download(yd, rows), ref)
+
+
+@pytest.mark.parametrize("wtype", [Q6_K, Q4_K])
+def test_feed_forward(backend, wtype):
+    rng = np.random.default_rng(23)
+    hidden, ffn = 4096, 12288
+    graw, uraw, draw = matrix(rng, wtype, ffn, hidden), matrix(rng, wtype, ffn, hidden), matrix(rng, Q6_K, hidden, ffn)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    g = backend.upload_weight(wtype, hidden, ffn, graw)
+    u = backend.upload_weight(wtype, hidden, ffn, uraw)
+    d = backend.upload_weight(Q6_K, ffn, hidden, draw)
+    xd, yd = backend.to_device(x), backend.alloc(hidden * 4)
+    backend.feed_forward(g, u, d, xd, yd)
+    got = backend.download(yd, hidden)
+    gr, ur = oracle.matvec(wtype, graw, x, ffn), oracle.matvec(wtype, uraw, x, ffn)
+    e = np.exp(-np.abs(gr))
+    s = np.where(gr >= 0, 1 / (1 + e), e / (1 + e)).astype(np.float32)
+    h = (gr * s * ur).astype(np.float32)
+    _close(got, oracle.matvec(Q6_K, draw, h, hidden))
+    for w in (g, u, d):
+        backend.weight_free(w)
+
+
+def _quantize_like_reference(x):
+    """core.cpp:119-125: x' = round(x/s) * fp16(s) per 32, s = amax/127."""
+    q = np.empty_like(x)
+    for s0 in range(0, x.size, 32):
+        blk = x[s0:s0 + 32]
+        s = np.float32(np.max(np.abs(blk)) / np.float32(127))
+        if s == 0:
+            q[s0:s0 + 32] = 0
+            continue
+        r = np.round(blk / s)
+        r = np.where(np.abs(blk / s - np.trunc(blk / s)) == 0.5, np.trunc(blk / s) + np.sign(blk), r)
+        q[s0:s0 + 32] = r.astype(np.float32) * np.float32(np.float16(s))
+    return q
+
+
+@pytest.mark.parametrize("rows,cols", [(256, 4096), (4096, 4096), (1024, 12288)])
+def test_q8_path(backend_q8, rows, cols):
+    raw, x, got = _run_linear(backend_q8, Q6_K, rows, cols, seed=rows + cols)
+    ref = oracle.matvec(Q6_K, raw, _quantize_like_reference(x), rows)
+    assert np.all(np.abs(got - ref) <= 1e-3 + 1e-4 * np.abs(ref)), np.max(np.abs(got - ref))
+    assert "Q8" in backend_q8.name
+
+
+def test_q8_leaves_q4k_on_fp32(backend_q8):
+    """--fast-q8 quantises activations for Q6_K only (cuda.cpp:709-718)."""
+    raw, x, y = _run_linear(backend_q8, Q4_K, 64, 4096, seed=77)
+    _close(y, oracle.matvec(Q4_K, raw, x, 64))
+
+
+def test_shape_errors(backend):
+    with pytest.raises(InvalidArgument):
+        backend.upload_weight(Q6_K, 255, 1, b"\0" * 210)
+    with pytest.raises(InvalidArgument):
+        backend.upload_weight(Q6_K, 256, 1, b"\0" * 209)
+    with pytest.raises(InvalidArgument):
+        backend.upload_weight(7, 256, 1, b"\0" * 1024)
+    w1 = backend.upload_weight(F32, 512, 2, np.zeros(1024, np.float32).tobytes())
+    w2 = backend.upload_weight(F32, 256, 2, np.zeros(512, np.float32).tobytes())
+    x, y = backend.alloc(4096), backend.alloc(4096)
+    with pytest.raises(InvalidArgument):
+        backend.linear_many([w1, w2], x, [y, y])
+    backend.weight_free(w1)
+    backend.weight_free(w2)
+
+
+def test_core_fp32_2x2(backend):
+    """core.cpp:92-98: [[1,2],[-3,4]] . [2,3] = [8,6] on the device."""
+    w = backend.upload_weight(F32, 2, 2, np.array([1, 2, -3, 4], np.float32).tobytes())
+    x, y = backend.to_device(np.array([2, 3], np.float32)), backend.alloc(8)
+    backend.linear(w, x, y)
+    assert backend.download(y, 2).tolist() == [8.0, 6.0]
+
+
+def test_budget_exhaustion():
+    from emprise_amd import ENOMEM, EmpriseError, HipBackend
+    with HipBackend(0, weight_budget=1000) as be:
+        with pytest.raises(EmpriseError) as e:
+            be.upload_weight(Q6_K, 4096, 1, b"\0" * 3360)
+        assert e.value.status == ENOMEM

@@ -1,0 +1,234 @@
+"""Decode-step mixer and small ops on the GPU through the C ABI, against the CPU oracle.
+
+Tolerance: max-abs error <= 1e-4 * max|ref| per FP32 output (north star); state
+buffers carried across several tokens are held to the same bar at every step.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from emprise_amd import (F32, Q4_K, Q6_K, AttentionParams, DeltaNetParams, Input, InvalidArgument,
+                         RecurrentParams)
+from synth import matrix
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(got, ref, tol=1e-4, what=""):
+    err = np.max(np.abs(got.astype(np.float64) - ref.astype(np.float64)))
+    bound = tol * max(np.max(np.abs(ref)), 1e-30)
+    assert err <= bound, f"{what} max abs err {err:.3e} > {bound:.3e}"
+
+
+def test_rmsnorm_add_swiglu(backend):
+    rng = np.random.default_rng(1)
+    n = 4096
+    x = rng.standard_normal(n).astype(np.float32) * 3
+    w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+    xd, wd, od = backend.to_device(x), backend.vector(w), backend.alloc(n * 4)
+    backend.rmsnorm(xd, wd, od, n, 1e-6)
+    _close(backend.download(od, n), oracle.rms(x, w, 1e-6))
+    y = rng.standard_normal(n).astype(np.float32)
+    yd = backend.to_device(y)
+    backend.add(xd, yd, n)
+    assert np.array_equal(backend.download(xd, n), x + y)
+    g = (rng.standard_normal(n) * 8).astype(np.float32)
+    gd = backend.to_device(g)
+    backend.swiglu(gd, yd, n)
+    ref = np.array([oracle.lib().eo_silu(float(v)) for v in g], dtype=np.float32) * y
+    _close(backend.download(gd, n), ref)
+
+
+@pytest.mark.parametrize("wtype,cols,rows", [(Q6_K, 4096, 151936), (Q6_K, 512, 4096), (Q4_K, 4096, 1000)])
+def test_embed_row(backend, wtype, cols, rows):
+    rng = np.random.default_rng(2)
+    raw = matrix(rng, wtype, rows, cols)
+    w = backend.upload_weight(wtype, cols, rows, raw)
+    rb = len(raw) // rows
+    out, tok = backend.alloc(cols * 4), backend.alloc(4)
+    for t in (0, rows // 3, rows - 1):
+        backend.upload(tok, np.array([t], np.int32))
+        backend.embed(w, tok, out)
+        ref = oracle.dequantize(wtype, raw[t * rb:(t + 1) * rb], cols)
+        assert np.array_equal(backend.download(out, cols).view(np.uint32), ref.view(np.uint32))
+    backend.weight_free(w)
+
+
+def test_argmax_first_maximum(backend):
+    rng = np.random.default_rng(4)
+    v = rng.standard_normal(151936).astype(np.float32)
+    v[[10, 5000, 90000]] = 9.0  # ties: std::max_element keeps the first
+    d, idx = backend.to_device(v), backend.alloc(4)
+    backend.argmax(d, v.size, idx)
+    assert backend.download(idx, 1, np.int32)[0] == 10
+    v2 = -np.abs(v) - 1
+    backend.upload(d, v2)
+    backend.argmax(d, v2.size, idx)
+    assert backend.download(idx, 1, np.int32)[0] == int(np.argmax(v2))
+
+
+def test_quantize_q8_matches_reference_rule(backend):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(4096).astype(np.float32)
+    x[64:96] = 0.0  # an all-zero block keeps scale 0 and codes 0
+    xd, qd, sd = backend.to_device(x), backend.alloc(4096), backend.alloc(4096 // 32 * 4)
+    backend.quantize_q8(xd, 4096, qd, sd)
+    q = backend.download(qd, 4096, np.int8)
+    s = backend.download(sd, 128)
+    for b in range(128):
+        blk = x[b * 32:(b + 1) * 32]
+        sc = np.float32(np.max(np.abs(blk)) / np.float32(127))
+        assert s[b] == np.float32(np.float16(sc))
+        if sc == 0:
+            assert np.all(q[b * 32:(b + 1) * 32] == 0)
+            continue
+        r = blk / sc
+        exp = np.where(np.abs(r - np.trunc(r)) == 0.5, np.trunc(r) + np.sign(r), np.round(r)).astype(np.int8)
+        assert np.array_equal(q[b * 32:(b + 1) * 32], exp)
+
+
+def _gdn_inputs(rng, kh, vh, sd, cw):
+    kd, vd = kh * sd, vh * sd
+    ch = 2 * kd + vd
+    return dict(
+        conv=(rng.standard_normal(ch * cw) * 0.5).astype(np.float32),
+        ssm_a=(-np.exp(rng.standard_normal(vh) * 0.5 - 2)).astype(np.float32),
+        dt=(rng.standard_normal(vh) * 0.5 - 1).astype(np.float32),
+        norm=(1 + 0.02 * rng.standard_normal(sd)).astype(np.float32),
+    )
+
+
+@pytest.mark.parametrize("kh,vh,sd,cw", [(16, 32, 128, 4), (4, 8, 64, 4)])
+def test_delta_net_steps(backend, kh, vh, sd, cw):
+    """Config 2a: GDN recurrent update over several tokens (state carried)."""
+    rng = np.random.default_rng(6)
+    kd, vd = kh * sd, vh * sd
+    ch = 2 * kd + vd
+    prm = _gdn_inputs(rng, kh, vh, sd, cw)
+    eps = 1e-6
+    conv_c = np.zeros(ch * cw, np.float32)
+    rec_c = np.zeros(vh * sd * sd, np.float32)
+    conv_g, rec_g = backend.to_device(conv_c), backend.to_device(rec_c)
+    wconv, wa, wdt, wn = (backend.vector(prm[k]) for k in ("conv", "ssm_a", "dt", "norm"))
+    bufs = {k: backend.alloc(n * 4) for k, n in (("qkv", ch), ("gate", vd), ("alpha", vh), ("beta", vh), ("out", vd))}
+    for step in range(5):
+        qkv = rng.standard_normal(ch).astype(np.float32)
+        gate = rng.standard_normal(vd).astype(np.float32)
+        alpha = rng.standard_normal(vh).astype(np.float32)
+        beta = rng.standard_normal(vh).astype(np.float32)
+        for k, v in (("qkv", qkv), ("gate", gate), ("alpha", alpha), ("beta", beta)):
+            backend.upload(bufs[k], v)
+        p = DeltaNetParams(kh, vh, sd, cw, eps, bufs["qkv"], bufs["gate"], bufs["alpha"], bufs["beta"], wconv, wa,
+                           wdt, wn, conv_g, rec_g, bufs["out"])
+        backend.delta_net(p)
+        ref = oracle.delta_net(kh, vh, sd, cw, eps, qkv, gate, alpha, beta, prm["conv"], prm["ssm_a"], prm["dt"],
+                               prm["norm"], conv_c, rec_c)
+        _close(backend.download(bufs["out"], vd), ref, what=f"step {step} out")
+        _close(backend.download(rec_g, vh * sd * sd), rec_c, what=f"step {step} state")
+        assert np.array_equal(backend.download(conv_g, ch * cw), conv_c)  # conv history is a copy
+
+
+@pytest.mark.parametrize("wtype", [Q6_K, Q4_K])
+def test_recurrent_block(backend, wtype):
+    """dev_recurrent: fused projections + conv epilogue + scan + out projection."""
+    rng = np.random.default_rng(7)
+    H, kh, vh, sd, cw, eps = 4096, 16, 32, 128, 4, 1e-6
+    kd, vd = kh * sd, vh * sd
+    ch = 2 * kd + vd
+    prm = _gdn_inputs(rng, kh, vh, sd, cw)
+    raws = {"qkv": (ch, H), "gate": (vd, H), "alpha": (vh, H), "beta": (vh, H), "out": (H, vd)}
+    raws = {k: (r, c, matrix(rng, wtype, r, c)) for k, (r, c) in raws.items()}
+    ws = {k: backend.upload_weight(wtype, c, r, raw) for k, (r, c, raw) in raws.items()}
+    wconv, wa, wdt, wn = (backend.vector(prm[k]) for k in ("conv", "ssm_a", "dt", "norm"))
+    conv_c, rec_c = np.zeros(ch * cw, np.float32), np.zeros(vh * sd * sd, np.float32)
+    conv_g, rec_g = backend.to_device(conv_c), backend.to_device(rec_c)
+    p = RecurrentParams(ws["qkv"], ws["gate"], ws["alpha"], ws["beta"], ws["out"], wconv, wa, wdt, wn, kh, vh, sd,
+                        cw, eps, conv_g, rec_g)
+    xd, yd = backend.alloc(H * 4), backend.alloc(H * 4)
+    for step in range(3):
+        x = rng.standard_normal(H).astype(np.float32)
+        backend.upload(xd, x)
+        backend.recurrent(p, xd, yd)
+        proj = {k: oracle.matvec(wtype, raws[k][2], x, raws[k][0]) for k in ("qkv", "gate", "alpha", "beta")}
+        dn = oracle.delta_net(kh, vh, sd, cw, eps, proj["qkv"], proj["gate"], proj["alpha"], proj["beta"],
+                              prm["conv"], prm["ssm_a"], prm["dt"], prm["norm"], conv_c, rec_c)
+        ref = oracle.matvec(wtype, raws["out"][2], dn, H)
+        _close(backend.download(yd, H), ref, tol=2e-4, what=f"step {step}")
+        _close(backend.download(rec_g, vh * sd * sd), rec_c, tol=2e-4, what=f"step {step} state")
+
+
+def _attention_case(backend, heads, kv, hd, rot, L, context, seed, base=1e7, eps=1e-6):
+    rng = np.random.default_rng(seed)
+    kvd = kv * hd
+    qn = (1 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+    keys = np.zeros((context, kvd), np.float32)
+    values = np.zeros((context, kvd), np.float32)
+    keys[:L - 1] = rng.standard_normal((L - 1, kvd)).astype(np.float32)
+    values[:L - 1] = rng.standard_normal((L - 1, kvd)).astype(np.float32)
+    qg = rng.standard_normal(heads * hd * 2).astype(np.float32)
+    k = rng.standard_normal(kvd).astype(np.float32)
+    v = rng.standard_normal(kvd).astype(np.float32)
+    kd_, vd_ = backend.to_device(keys), backend.to_device(values)
+    qkv = backend.to_device(np.concatenate([qg, k, v]))
+    pos = backend.to_device(np.array([L - 1], np.int32))
+    out = backend.alloc(heads * hd * 4)
+    p = AttentionParams(heads, kv, hd, rot, context, eps, base, backend.vector(qn), backend.vector(kn), kd_, vd_, pos)
+    backend.attention(p, qkv, out)
+    got = backend.download(out, heads * hd)
+    ref = oracle.attention(heads, kv, hd, rot, base, eps, qn, kn, qg, k, v, keys, values, L, L - 1)
+    _close(got, ref, what=f"L={L}")
+    # the new k/v landed at row L-1 of the caches
+    _close(backend.download(kd_, (context, kvd))[L - 1], keys[L - 1])
+    assert np.array_equal(backend.download(vd_, (context, kvd))[L - 1], v)
+    for b in (kd_, vd_, qkv, pos, out):
+        backend.free(b)
+
+
+@pytest.mark.parametrize("L", [1, 2, 63, 64, 65, 512, 2048, 4096])
+def test_attention_config2b(backend, L):
+    """Config 2b: 16 Q / 4 KV heads, head_dim 256, partial RoPE over 64 dims."""
+    _attention_case(backend, 16, 4, 256, 64, L, 4096, seed=L)
+
+
+@pytest.mark.parametrize("L", [1, 7, 130])
+def test_attention_tiny(backend, L):
+    _attention_case(backend, 8, 2, 64, 16, L, 512, seed=100 + L)
+
+
+def test_attention_rejects_bad_shape(backend):
+    p = AttentionParams(16, 5, 256, 64, 64, 1e-6, 1e7, backend.vector(np.ones(256, np.float32)),
+                        backend.vector(np.ones(256, np.float32)), 1, 1, 1)
+    with pytest.raises(InvalidArgument):
+        backend.attention(p, 1, 1)
+
+
+def test_graph_replay_matches_eager(backend):
+    """A captured linear_norm + argmax sequence replayed several times (with eager
+    work between replays) gives the eager result each time."""
+    rng = np.random.default_rng(9)
+    cols, rows = 4096, 20000
+    raw = matrix(rng, Q6_K, rows, cols)
+    w = backend.upload_weight(Q6_K, cols, rows, raw)
+    nw = backend.vector((1 + 0.02 * rng.standard_normal(cols)).astype(np.float32))
+    xd, dd, xo, yd, idx = (backend.alloc(cols * 4), backend.alloc(cols * 4), backend.alloc(cols * 4),
+                           backend.alloc(rows * 4), backend.alloc(4))
+    inp = Input(xd, dd, xo, nw, 1e-6)
+    backend.upload(xd, rng.standard_normal(cols).astype(np.float32))
+    backend.upload(dd, rng.standard_normal(cols).astype(np.float32))
+    backend.linear_norm(inp, [w], [yd])
+    backend.argmax(yd, rows, idx)
+    eager_y, eager_i = backend.download(yd, rows), backend.download(idx, 1, np.int32)
+    backend.graph_begin()
+    backend.linear_norm(inp, [w], [yd])
+    backend.argmax(yd, rows, idx)
+    g = backend.graph_end()
+    for _ in range(4):
+        backend.fill(yd, 0.0, rows)
+        backend.upload(idx, np.array([-1], np.int32))
+        backend.graph_launch(g)
+        backend.sync()
+        assert np.array_equal(backend.download(yd, rows), eager_y)
+        assert backend.download(idx, 1, np.int32)[0] == eager_i[0]
+    backend.graph_destroy(g)
+    backend.weight_free(w)
