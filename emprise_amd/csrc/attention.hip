@@ -39,7 +39,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     const int len = pos + 1;
     const int nchunks = (len + CH - 1) / CH;
     if (chunk >= nchunks) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int qd = a.heads * HD * 2, kvd = a.kv_heads * HD;
     const float* kin = a.qkv + qd + (size_t)kvh * HD;
     const float* vin = a.qkv + qd + kvd + (size_t)kvh * HD;

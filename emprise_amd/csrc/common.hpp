@@ -23,16 +23,33 @@ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
     return bits;
 }
 
+// Wave64 reductions on DPP lane shifts (ALU only, no LDS round trips): inclusive
+// prefix within each row of 16 lanes (row_shr 1, 2, 4, 8), then row_bcast:15 and
+// row_bcast:31 carry the row totals up to lane 63, which is broadcast to the wave.
+// Lanes whose DPP source is out of range keep `old` (0 for sums, the value for max).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+    v += dpp_f<0x111, 0xf>(0.f, v);  // row_shr:1
+    v += dpp_f<0x112, 0xf>(0.f, v);  // row_shr:2
+    v += dpp_f<0x114, 0xf>(0.f, v);  // row_shr:4
+    v += dpp_f<0x118, 0xf>(0.f, v);  // row_shr:8
+    v += dpp_f<0x142, 0xa>(0.f, v);  // row_bcast:15 into rows 1, 3
+    v += dpp_f<0x143, 0xc>(0.f, v);  // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
+    v = fmaxf(v, dpp_f<0x111, 0xf>(v, v));
+    v = fmaxf(v, dpp_f<0x112, 0xf>(v, v));
+    v = fmaxf(v, dpp_f<0x114, 0xf>(v, v));
+    v = fmaxf(v, dpp_f<0x118, 0xf>(v, v));
+    v = fmaxf(v, dpp_f<0x142, 0xa>(v, v));
+    v = fmaxf(v, dpp_f<0x143, 0xc>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` holds >= 16 floats.

@@ -39,7 +39,7 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_kernel(GdnArgs a) {
     __shared__ float o_row[SD];
     const int h = blockIdx.x, kh = h % a.key_heads;  // tiled V-head order (backend.cpp:37)
     const int key_dim = a.key_heads * SD;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const float* q = a.qkv + (size_t)kh * SD;
     const float* k = a.qkv + key_dim + (size_t)kh * SD;
     const float* v = a.qkv + 2 * (size_t)key_dim + (size_t)h * SD;

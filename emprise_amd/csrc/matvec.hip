@@ -78,6 +78,39 @@ __device__ void stage_q8(int n, const float* xs, int8_t* xq, float* xscale, int*
     }
 }
 
+// The same quantisation with eight values per thread: the four threads of a 32-value
+// block combine their maxima with xor-shuffles inside a quad, then each rounds its own
+// eight values. Requires n % 2048 == 0 so every lane of the block has work.
+__device__ void stage_q8_wide(int n, const float* xs, int8_t* xq, float* xscale, int* qsum) {
+    for (int e = threadIdx.x; e < n / 8; e += blockDim.x) {
+        const float4 v0 = reinterpret_cast<const float4*>(xs)[2 * e];
+        const float4 v1 = reinterpret_cast<const float4*>(xs)[2 * e + 1];
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        const float s = amax / 127.f;
+        int q[8], part = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            q[i] = s != 0.f ? (int)roundf(v[i] / s) : 0;
+            part += q[i];
+        }
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo |= (uint32_t)(q[i] & 0xff) << (8 * i);
+            hi |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
+        }
+        reinterpret_cast<uint2*>(xq)[e] = make_uint2(lo, hi);
+        part += __shfl_xor(part, 1, 64);  // the two threads of one 16-value unit
+        if ((e & 1) == 0) qsum[e >> 1] = part;
+        if ((e & 3) == 0) xscale[e >> 2] = half_bits_to_float(float_to_half_bits(s));
+    }
+}
+
 // ---- per-unit dot products --------------------------------------------------------
 
 __device__ __forceinline__ float dot4(uint32_t q, const float4& x, float acc) {
@@ -88,10 +121,18 @@ __device__ __forceinline__ float dot4(uint32_t q, const float4& x, float acc) {
     return acc;
 }
 
+// Hides a value's known-zero bits from the optimiser, so byte-to-float conversions of
+// masked codes select v_cvt_f32_ubyte{0..3} (one instruction per weight) instead of a
+// bit-field extract plus a conversion.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // sum over the 16 codes of a Q6_K unit times x (codes 0..63, no zero point)
 __device__ __forceinline__ float q6_unit(uint32_t d0, uint32_t d1, uint32_t d2, const float4* x) {
-    const uint32_t a = d0 & 0x3F3F3F3Fu, b = d1 & 0x3F3F3F3Fu, c = d2 & 0x3F3F3F3Fu;
-    const uint32_t e = ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u);
+    const uint32_t a = opaque(d0 & 0x3F3F3F3Fu), b = opaque(d1 & 0x3F3F3F3Fu), c = opaque(d2 & 0x3F3F3F3Fu);
+    const uint32_t e = opaque(((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u));
     float s0 = dot4(a, x[0], 0.f);
     float s1 = dot4(b, x[1], 0.f);
     s0 = dot4(c, x[2], s0);
@@ -101,14 +142,14 @@ __device__ __forceinline__ float q6_unit(uint32_t d0, uint32_t d1, uint32_t d2, 
 
 // sum over the 32 codes of a Q4_K unit times x
 __device__ __forceinline__ float q4_unit(const uint4& d, const float4* x) {
-    float s0 = dot4(d.x & 0x0F0F0F0Fu, x[0], 0.f);
-    float s1 = dot4(d.y & 0x0F0F0F0Fu, x[1], 0.f);
-    s0 = dot4(d.z & 0x0F0F0F0Fu, x[2], s0);
-    s1 = dot4(d.w & 0x0F0F0F0Fu, x[3], s1);
-    s0 = dot4((d.x >> 4) & 0x0F0F0F0Fu, x[4], s0);
-    s1 = dot4((d.y >> 4) & 0x0F0F0F0Fu, x[5], s1);
-    s0 = dot4((d.z >> 4) & 0x0F0F0F0Fu, x[6], s0);
-    s1 = dot4((d.w >> 4) & 0x0F0F0F0Fu, x[7], s1);
+    float s0 = dot4(opaque(d.x & 0x0F0F0F0Fu), x[0], 0.f);
+    float s1 = dot4(opaque(d.y & 0x0F0F0F0Fu), x[1], 0.f);
+    s0 = dot4(opaque(d.z & 0x0F0F0F0Fu), x[2], s0);
+    s1 = dot4(opaque(d.w & 0x0F0F0F0Fu), x[3], s1);
+    s0 = dot4(opaque((d.x >> 4) & 0x0F0F0F0Fu), x[4], s0);
+    s1 = dot4(opaque((d.y >> 4) & 0x0F0F0F0Fu), x[5], s1);
+    s0 = dot4(opaque((d.z >> 4) & 0x0F0F0F0Fu), x[6], s0);
+    s1 = dot4(opaque((d.w >> 4) & 0x0F0F0F0Fu), x[7], s1);
     return s0 + s1;
 }
 
@@ -202,7 +243,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
     if (a.mode == kMvArgmax && threadIdx.x == 0) block_best = 0ull;
     __syncthreads();
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nb = a.cols / 256;
     const size_t row_bytes = (size_t)nb * Fmt<T>::block;
     constexpr int NA = PAIR ? R * 2 : R;  // accumulators (pair mode: R gate + R up rows)
@@ -271,6 +312,337 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
     }
 }
 
+// ---- streaming kernel for inputs that are a multiple of 4096 wide ------------------------
+//
+// Same lane -> unit mapping as above, but each wave walks a sequence of (row group,
+// 4096-column chunk) items and keeps the next item's weights in flight while it computes
+// the current one: the loads of item i+1 are issued before the arithmetic of item i,
+// and the very first item's loads are issued before the workgroup stages its input.
+// A chunk holds 64 weights per lane per row: 4 Q6_K units (12 B codes + scale + d each)
+// or 2 Q4_K units (16 B nibbles + 3 scale bytes + d/dmin each).
+
+template <int T, int NA> struct Chunk;
+template <int NA> struct Chunk<kQ6K, NA> {
+    uint32_t q[NA][4][3];
+    int32_t sc[NA][4];
+    uint32_t d[NA][4];
+};
+template <int NA> struct Chunk<kQ4K, NA> {
+    uint4 q[NA][2];
+    uint32_t b0[NA][2], b1[NA][2], b2[NA][2];  // scale bytes A, B, C (see q4_lane_scale)
+    uint32_t dd[NA][2];                        // fp16 d | fp16 dmin << 16
+};
+
+// Q4_K scale/min of sub-block j from three bytes: for j < 4, A = s[j], B = s[j+4];
+// for j >= 4, A = s[j+4], B = s[j-4], C = s[j] (quant.cpp:48-52).
+__device__ __forceinline__ void q4_offsets(int j, int& oa, int& ob, int& oc) {
+    oa = j < 4 ? j : j + 4;
+    ob = j < 4 ? j + 4 : j - 4;
+    oc = j;
+}
+__device__ __forceinline__ void q4_lane_scale(int j, uint32_t A, uint32_t B, uint32_t C, int& sc, int& mn) {
+    if (j < 4) {
+        sc = A & 63;
+        mn = B & 63;
+    } else {
+        sc = (A & 15) | ((B >> 6) << 4);
+        mn = (A >> 4) | ((C >> 6) << 4);
+    }
+}
+
+template <int T, int NA>
+__device__ __forceinline__ void load_chunk(Chunk<T, NA>& ch, const uint8_t* const* rp, int nb, int c, int lane) {
+    if constexpr (T == kQ6K) {
+#pragma unroll
+        for (int r = 0; r < NA; ++r)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int u = c * 256 + lane + 64 * k;
+                const uint8_t* q = rp[r] + (size_t)u * 12;
+                ch.q[r][k][0] = ld_u32(q);
+                ch.q[r][k][1] = ld_u32(q + 4);
+                ch.q[r][k][2] = ld_u32(q + 8);
+                ch.sc[r][k] = (int8_t)rp[r][(size_t)nb * 192 + u];
+                ch.d[r][k] = *reinterpret_cast<const uint16_t*>(rp[r] + (size_t)nb * 208 + 2 * (u >> 4));
+            }
+    } else {
+        int oa, ob, oc;
+        q4_offsets(lane & 7, oa, ob, oc);
+#pragma unroll
+        for (int r = 0; r < NA; ++r)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int u = c * 128 + lane + 64 * k;
+                ch.q[r][k] = *reinterpret_cast<const uint4*>(rp[r] + (size_t)u * 16);
+                const uint8_t* s = rp[r] + (size_t)nb * 128 + (size_t)(u >> 3) * 12;
+                ch.b0[r][k] = s[oa];
+                ch.b1[r][k] = s[ob];
+                ch.b2[r][k] = s[oc];
+                ch.dd[r][k] = *reinterpret_cast<const uint32_t*>(rp[r] + (size_t)nb * 140 + (size_t)(u >> 3) * 4);
+            }
+    }
+}
+
+template <int T, int NA>
+__device__ __forceinline__ void compute_chunk(const Chunk<T, NA>& ch, float* acc, const float* xs, const float* usum,
+                                              int c, int lane) {
+    if constexpr (T == kQ6K) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int u = c * 256 + lane + 64 * k;
+            float4 xv[4];
+            const float4* xp = reinterpret_cast<const float4*>(xs) + (size_t)((c * 4 + k) * 4) * 64 + lane;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[i] = xp[i * 64];
+            const float xsum = usum[u];
+#pragma unroll
+            for (int r = 0; r < NA; ++r) {
+                const float s = q6_unit(ch.q[r][k][0], ch.q[r][k][1], ch.q[r][k][2], xv);
+                const float d = half_bits_to_float((uint16_t)ch.d[r][k]);
+                acc[r] = fmaf(d * (float)ch.sc[r][k], fmaf(-32.f, xsum, s), acc[r]);
+            }
+        }
+    } else {
+        const int j = lane & 7;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int u = c * 128 + lane + 64 * k;
+            float4 xv[8];
+            const float4* xp = reinterpret_cast<const float4*>(xs) + (size_t)((c * 2 + k) * 8) * 64 + lane;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = xp[i * 64];
+            const float xsum = usum[u];
+#pragma unroll
+            for (int r = 0; r < NA; ++r) {
+                int sc, mn;
+                q4_lane_scale(j, ch.b0[r][k], ch.b1[r][k], ch.b2[r][k], sc, mn);
+                const float dd = half_bits_to_float((uint16_t)(ch.dd[r][k] & 0xffff));
+                const float dm = half_bits_to_float((uint16_t)(ch.dd[r][k] >> 16));
+                const float s = q4_unit(ch.q[r][k], xv);
+                acc[r] += (dd * (float)sc) * s - (dm * (float)mn) * xsum;
+            }
+        }
+    }
+}
+
+// Q8 activations (Q6_K only): integer dot of the codes with the int8 input per unit.
+template <int NA>
+__device__ __forceinline__ void compute_chunk_q8(const Chunk<kQ6K, NA>& ch, float* acc, const int8_t* xq,
+                                                 const float* xscale, const int* qsum, int c, int lane) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int u = c * 256 + lane + 64 * k;
+        const int4 xv = *reinterpret_cast<const int4*>(xq + (size_t)u * 16);
+        const int q32 = 32 * qsum[u];
+        const float s8 = xscale[u >> 1];
+#pragma unroll
+        for (int r = 0; r < NA; ++r) {
+            const uint32_t d0 = ch.q[r][k][0], d1 = ch.q[r][k][1], d2 = ch.q[r][k][2];
+            const uint32_t e = ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u);
+            int dot = __builtin_amdgcn_sdot4((int)(d0 & 0x3F3F3F3Fu), xv.x, 0, false);
+            dot = __builtin_amdgcn_sdot4((int)(d1 & 0x3F3F3F3Fu), xv.y, dot, false);
+            dot = __builtin_amdgcn_sdot4((int)(d2 & 0x3F3F3F3Fu), xv.z, dot, false);
+            dot = __builtin_amdgcn_sdot4((int)e, xv.w, dot, false);
+            const float d = half_bits_to_float((uint16_t)ch.d[r][k]);
+            acc[r] += ((float)(dot - q32) * (d * (float)ch.sc[r][k])) * s8;
+        }
+    }
+}
+
+// LDS slot of input float4 i. Interleaved (PERM): the float4s of 64 consecutive units
+// are stored lane-major -- float4 j of unit u at ((u/64)*(unit/4) + j)*64 + u%64 -- so
+// when lane l reads unit base+l every lane hits the next 16 bytes (no bank conflicts).
+template <bool PERM, int UNIT> __device__ __forceinline__ int xslot(int i) {
+    if constexpr (!PERM) return i;
+    constexpr int U4 = UNIT / 4;
+    const int u = i / U4, j = i % U4;
+    return ((u >> 6) * U4 + j) * 64 + (u & 63);
+}
+
+// Input staging with 16-byte loads, four in flight per thread.
+template <bool PERM, int UNIT>
+__device__ void stage_input_wide(const MvArgs& a, float* xs, float* usum, float* red) {
+    constexpr int unit = UNIT;
+    const int n4 = a.cols / 4;
+    const bool writer = a.x_out && blockIdx.x == 0;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    const float4* d4 = reinterpret_cast<const float4*>(a.delta);
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+    float ss = 0.f;
+    for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * blockDim.x) {
+        float4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = i0 + k * blockDim.x;
+            if (i < n4) {
+                v[k] = x4[i];
+                if (d4) {
+                    const float4 dv = d4[i];
+                    v[k].x += dv.x;
+                    v[k].y += dv.y;
+                    v[k].z += dv.z;
+                    v[k].w += dv.w;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = i0 + k * blockDim.x;
+            if (i < n4) {
+                if (writer) reinterpret_cast<float4*>(a.x_out)[i] = v[k];
+                xs4[xslot<PERM, UNIT>(i)] = v[k];
+                ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+            }
+        }
+    }
+    if (a.norm) {
+        const float total = block_sum(ss, red);
+        const float scale = 1.f / sqrtf(total / (float)a.cols + a.eps);
+        const float4* n4p = reinterpret_cast<const float4*>(a.norm);
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * blockDim.x) {
+            float4 w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (i0 + k * (int)blockDim.x < n4) w[k] = n4p[i0 + k * blockDim.x];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int i = i0 + k * blockDim.x;
+                if (i < n4) {
+                    const int sl = xslot<PERM, UNIT>(i);
+                    float4 v = xs4[sl];
+                    v.x = v.x * (scale * w[k].x);
+                    v.y = v.y * (scale * w[k].y);
+                    v.z = v.z * (scale * w[k].z);
+                    v.w = v.w * (scale * w[k].w);
+                    xs4[sl] = v;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int units = a.cols / unit;
+    for (int u = threadIdx.x; u < units; u += blockDim.x) {
+        float s = 0.f;
+        for (int j = 0; j < unit / 4; ++j) {
+            const float4 v = xs4[xslot<PERM, UNIT>(u * (unit / 4) + j)];
+            s += (v.x + v.y) + (v.z + v.w);
+        }
+        usum[u] = s;
+    }
+}
+
+template <int T, int R, bool Q8, bool PAIR>
+__global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float red[16];
+    __shared__ unsigned long long block_best;
+    constexpr int UW = Fmt<T>::unit;
+    constexpr int NA = PAIR ? R * 2 : R;
+    float* xs = reinterpret_cast<float*>(smem);
+    float* usum = xs + a.cols;
+    const int units = a.cols / UW;
+    int8_t* xq = reinterpret_cast<int8_t*>(usum + units);
+    float* xscale = reinterpret_cast<float*>(xq + a.cols);
+    int* qsum = reinterpret_cast<int*>(xscale + a.cols / 32);
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = a.cols / 256;
+    const int cpr = a.cols / 4096;  // chunks per row
+    const size_t row_bytes = (size_t)nb * Fmt<T>::block;
+    const int stride = gridDim.x * 4;
+
+    // row pointers of group g (clamped to the segment's last row)
+    auto rows_of = [&](int g, const uint8_t** rp, int& s, int& row0) {
+        s = 0;
+        while (s + 1 < a.nseg && g >= a.seg[s + 1].g0) ++s;
+        row0 = (g - a.seg[s].g0) * R;
+        const int nrows = a.seg[s].rows;
+#pragma unroll
+        for (int r = 0; r < NA; ++r) {
+            const int rr = r < R ? row0 + r : row0 + r - R;
+            const int rc = rr < nrows ? rr : nrows - 1;
+            rp[r] = (r < R ? a.seg[s].w : a.seg[1].w) + (size_t)rc * row_bytes;
+        }
+    };
+
+    int g = blockIdx.x * 4 + wave, c = 0;
+    const uint8_t* rp[NA];
+    int seg = 0, row0 = 0;
+    Chunk<T, NA> cur, nxt;
+    if (g < a.groups) {
+        rows_of(g, rp, seg, row0);
+        load_chunk<T, NA>(cur, rp, nb, 0, lane);
+    }
+    stage_input_wide<!Q8, UW>(a, xs, usum, red);
+    if constexpr (Q8) {
+        __syncthreads();
+        stage_q8_wide(a.cols, xs, xq, xscale, qsum);
+    }
+    if (a.mode == kMvArgmax && threadIdx.x == 0) block_best = 0ull;
+    __syncthreads();
+
+    unsigned long long best = 0ull;
+    float acc[NA];
+#pragma unroll
+    for (int r = 0; r < NA; ++r) acc[r] = 0.f;
+    while (g < a.groups) {
+        int gn = g, cn = c + 1;
+        if (cn == cpr) {
+            cn = 0;
+            gn = g + stride;
+        }
+        const uint8_t* rpn[NA];
+        int segn = seg, row0n = row0;
+        if (gn < a.groups) {
+            if (gn != g) rows_of(gn, rpn, segn, row0n);
+            else
+#pragma unroll
+                for (int r = 0; r < NA; ++r) rpn[r] = rp[r];
+            load_chunk<T, NA>(nxt, rpn, nb, cn, lane);
+        }
+        if constexpr (Q8) compute_chunk_q8<NA>(cur, acc, xq, xscale, qsum, c, lane);
+        else compute_chunk<T, NA>(cur, acc, xs, usum, c, lane);
+        if (c == cpr - 1) {
+#pragma unroll
+            for (int r = 0; r < NA; ++r) acc[r] = wave_sum(acc[r]);
+            if (lane == 0) {
+                const MvSeg sg = a.seg[seg];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int row = row0 + r;
+                    if (row < sg.rows) {
+                        if constexpr (PAIR) {
+                            sg.y[row] = siluf_(acc[r]) * acc[(R + r) % NA];
+                        } else if (a.conv_w && seg == 0) {
+                            sg.y[row] = conv_step(a.conv_w, a.conv_state, a.conv_width, row, acc[r]);
+                        } else {
+                            sg.y[row] = acc[r];
+                            if (a.mode == kMvArgmax) {
+                                const unsigned long long k = argmax_key(acc[r], row);
+                                best = k > best ? k : best;
+                            }
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < NA; ++r) acc[r] = 0.f;
+        }
+        cur = nxt;
+        g = gn;
+        c = cn;
+        seg = segn;
+        row0 = row0n;
+#pragma unroll
+        for (int r = 0; r < NA; ++r) rp[r] = rpn[r];
+    }
+    if (a.mode == kMvArgmax) {
+        if (lane == 0 && best) atomicMax(&block_best, best);
+        __syncthreads();
+        if (threadIdx.x == 0 && block_best) atomicMax(a.argmax, block_best);
+    }
+}
+
 // Plain-layout (F32 / F16 / BF16) matvec: one wave per row, lanes stride the columns.
 template <int T>
 __device__ __forceinline__ float raw_elem(const uint8_t* row, int k) {
@@ -289,7 +661,7 @@ __global__ __launch_bounds__(256) void matvec_raw_kernel(MvArgs a) {
     stage_input(a, xs, usum, 1 << 30, red);  // no unit sums needed
     if (a.mode == kMvArgmax && threadIdx.x == 0) block_best = 0ull;
     __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const size_t row_bytes = (size_t)a.cols * (T == kF32 ? 4 : 2);
     const bool pair = a.mode == kMvSwiglu;
     unsigned long long best = 0ull;
@@ -348,6 +720,34 @@ size_t matvec_lds_bytes(uint32_t type, int cols, bool q8) {
     return (size_t)cols * 4 + 16;
 }
 
+// Workgroups of a streaming launch: one full round of resident workgroups (occupancy x
+// CUs), so every wave keeps two items in flight and none waits for a second round.
+// EMPRISE_MV_WAVES_PER_CU (resident waves per CU to aim for) overrides it for sweeps.
+template <class K> static int resident_blocks(K kernel, size_t lds) {
+    static int cached = 0;
+    if (!cached) {
+        int dev = 0, per_cu = 0;
+        hipDeviceProp_t prop;
+        (void)hipGetDevice(&dev);
+        (void)hipGetDeviceProperties(&prop, dev);
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), 256, lds);
+        const char* e = getenv("EMPRISE_MV_WAVES_PER_CU");
+        const int want = e ? atoi(e) / 4 : 0;
+        if (want > 0 && want < per_cu) per_cu = want;
+        cached = (per_cu > 0 ? per_cu : 1) * prop.multiProcessorCount;
+    }
+    return cached;
+}
+
+template <class K> static hipError_t launch_stream(K kernel, const MvArgs& a, size_t lds, hipStream_t stream) {
+    int blocks = (a.groups + 3) / 4;
+    const int cap = resident_blocks(kernel, lds);
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), lds, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, hipStream_t stream) {
     const size_t lds = matvec_lds_bytes(type, a.cols, q8);
     int blocks = (a.groups + 3) / 4;
@@ -355,6 +755,16 @@ hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, 
     if (blocks < 1) blocks = 1;
     const dim3 grid(blocks), block(256);
     const bool pair = a.mode == kMvSwiglu;
+    if ((type == kQ6K || type == kQ4K) && a.cols % 4096 == 0) {
+        if (type == kQ6K) {
+            if (q8) return pair ? launch_stream(matvec_stream_kernel<kQ6K, kMvRows, true, true>, a, lds, stream)
+                                : launch_stream(matvec_stream_kernel<kQ6K, kMvRows, true, false>, a, lds, stream);
+            return pair ? launch_stream(matvec_stream_kernel<kQ6K, kMvRows, false, true>, a, lds, stream)
+                        : launch_stream(matvec_stream_kernel<kQ6K, kMvRows, false, false>, a, lds, stream);
+        }
+        return pair ? launch_stream(matvec_stream_kernel<kQ4K, kMvRows, false, true>, a, lds, stream)
+                    : launch_stream(matvec_stream_kernel<kQ4K, kMvRows, false, false>, a, lds, stream);
+    }
     switch (type) {
     case kQ6K:
         if (q8) {

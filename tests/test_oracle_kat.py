@@ -1,0 +1,125 @@
+"""The reference's own known-answer tests (v1.1 tests/core.cpp) restated against the
+CPU oracle, plus closed-form checks of the quant formats. CPU only."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import BF16, F16, F32, Q4_K, Q6_K
+from synth import decode_q4k_block, decode_q6k_block, encode_q6k_block, q4k_blocks, q6k_blocks
+
+
+def test_half_to_float_core_cases():
+    """core.cpp:42-47."""
+    h = oracle.half_to_float
+    assert h(0x3C00) == 1.0
+    assert h(0xC000) == -2.0
+    assert h(1) == math.ldexp(1.0, -24)
+    assert math.copysign(1.0, h(0x8000)) == -1.0 and h(0x8000) == 0.0
+    assert math.isinf(h(0x7C00))
+    assert math.isnan(h(0x7E00))
+
+
+def test_half_to_float_all_inputs_match_ieee():
+    """Every fp16 bit pattern against numpy's IEEE half conversion."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.half_to_float(int(b)) for b in bits], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_encoded_size_rejections():
+    """core.cpp:48-49: Q6_K needs whole 256-blocks; overflowing sizes are rejected."""
+    L = oracle.lib()
+    assert L.eo_encoded_bytes(Q6_K, 255) == 0
+    assert L.eo_encoded_bytes(F32, 2 ** 64 - 1) == 0
+    assert L.eo_encoded_bytes(Q6_K, 512) == 420 and L.eo_encoded_bytes(Q4_K, 512) == 288
+    assert L.eo_encoded_bytes(7, 256) == 0
+
+
+def _core_q6k_block():
+    """The independently encoded block of core.cpp:51-65: q=(i*13+7)%64, scales i-8, d=0.5."""
+    q = np.array([(i * 13 + 7) % 64 for i in range(256)])
+    blk = encode_q6k_block(q, np.arange(16) - 8, 0x3800)
+    expected = np.array([0.5 * (i // 16 - 8) * (q[i] - 32) for i in range(256)], dtype=np.float32)
+    x = np.array([(i % 7) - 3 for i in range(256)], dtype=np.float32)
+    return blk, expected, x
+
+
+def test_core_q6k_block_exact():
+    """core.cpp:66-72: exact dequantisation and an exact 256-term dot."""
+    blk, expected, x = _core_q6k_block()
+    got = oracle.dequantize(Q6_K, blk.tobytes(), 256)
+    assert np.array_equal(got, expected)
+    dot = np.float32(0)
+    for i in range(256):
+        dot = np.float32(dot + expected[i] * x[i])
+    assert oracle.matvec(Q6_K, blk.tobytes(), x, 1)[0] == dot
+    with pytest.raises(ValueError):
+        oracle.dequantize(Q6_K, blk.tobytes()[:209], 256)
+
+
+def test_core_fp32_matvec():
+    """core.cpp:92-94: [[1,2],[-3,4]] . [2,3] = [8,6]."""
+    w = np.array([1, 2, -3, 4], dtype=np.float32).tobytes()
+    assert oracle.matvec(F32, w, np.array([2, 3], np.float32), 2).tolist() == [8.0, 6.0]
+
+
+def test_q6k_random_blocks_match_independent_decoder():
+    rng = np.random.default_rng(0)
+    blocks = q6k_blocks(rng, 40)
+    got = oracle.dequantize(Q6_K, blocks.tobytes(), 40 * 256).reshape(40, 256)
+    for b in range(40):
+        want = decode_q6k_block(blocks[b])
+        # (d*sc)*q is exact in FP32, so the float64 value is hit exactly
+        assert np.array_equal(got[b].astype(np.float64), want)
+
+
+def test_q4k_random_blocks_match_independent_decoder():
+    """No reference test covers Q4_K: pin against the GGUF definition in float64; the
+    FP32 result (d*sc)*q - dmin*m has one rounding, at the subtraction."""
+    rng = np.random.default_rng(1)
+    blocks = q4k_blocks(rng, 40)
+    got = oracle.dequantize(Q4_K, blocks.tobytes(), 40 * 256).reshape(40, 256)
+    for b in range(40):
+        want = decode_q4k_block(blocks[b]).astype(np.float32)
+        assert np.array_equal(got[b], want)
+
+
+def test_f16_bf16_dequantize():
+    rng = np.random.default_rng(2)
+    v = rng.standard_normal(512).astype(np.float32)
+    h = v.astype(np.float16)
+    assert np.array_equal(oracle.dequantize(F16, h.tobytes(), 512), h.astype(np.float32))
+    b = (v.view(np.uint32) >> 16).astype(np.uint16)
+    want = (b.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(oracle.dequantize(BF16, b.tobytes(), 512), want)
+
+
+@pytest.mark.parametrize("wtype", [Q6_K, Q4_K])
+def test_matvec_is_sequential_fp32_row_sum(wtype):
+    """quant.cpp:91-97: each row is one FP32 accumulator summed in element order."""
+    rng = np.random.default_rng(3)
+    rows, cols = 5, 512
+    raw = (q6k_blocks if wtype == Q6_K else q4k_blocks)(rng, rows * cols // 256).tobytes()
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = oracle.dequantize(wtype, raw, rows * cols).reshape(rows, cols)
+    got = oracle.matvec(wtype, raw, x, rows)
+    for r in range(rows):
+        s = np.float32(0)
+        for k in range(cols):
+            s = np.float32(s + np.float32(w[r, k] * x[k]))
+        assert got[r] == s
+    # and within FP32 rounding of the float64 brute force
+    exact = w.astype(np.float64) @ x.astype(np.float64)
+    assert np.max(np.abs(got - exact)) <= 1e-5 * np.max(np.abs(exact))
+
+
+def test_matvec_rejects_mismatched_sizes():
+    with pytest.raises(ValueError):
+        oracle.matvec(Q6_K, b"\0" * 211, np.zeros(256, np.float32), 1)
+    with pytest.raises(ValueError):
+        oracle.matvec(Q6_K, b"\0" * 420, np.zeros(256, np.float32), 3)

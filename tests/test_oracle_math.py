@@ -1,0 +1,173 @@
+"""Closed forms and invariants that pin the oracle functions the reference's compiled
+code does not expose (RMSNorm, RoPE and attention live in model.cpp's private
+Model::Impl). Each check is chosen so a dropped term, wrong sign/index or transposed
+operand fails it. CPU only."""
+import numpy as np
+
+import oracle
+
+
+def test_rms_closed_form():
+    x = np.array([3.0, 4.0], np.float32)
+    w = np.array([1.0, 2.0], np.float32)
+    got = oracle.rms(x, w, 0.0)
+    s = 1 / np.sqrt(12.5)  # mean of squares (9 + 16) / 2
+    assert np.allclose(got, [3 * s, 8 * s], rtol=1e-7)
+    # eps enters under the root, not outside
+    assert np.allclose(oracle.rms(np.zeros(4, np.float32), np.ones(4, np.float32), 1.0), 0)
+    assert np.allclose(oracle.rms(np.ones(4, np.float32), np.ones(4, np.float32), 3.0), 0.5)
+
+
+def test_rope_identity_at_position_zero_and_norm_preserving():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(64).astype(np.float32)
+    assert np.array_equal(oracle.rope(x, 16, 0, 1e7), x)
+    y = oracle.rope(x, 16, 37, 1e7)
+    # rotation of pairs (i, i+8) for i < 8; the other 48 dims untouched
+    assert np.array_equal(y[16:], x[16:])
+    for i in range(8):
+        a, b = x[i], x[i + 8]
+        assert abs(np.hypot(y[i], y[i + 8]) - np.hypot(a, b)) < 1e-5
+        ang = 37 / np.power(1e7, 2 * i / 16)
+        assert np.allclose([y[i], y[i + 8]], [a * np.cos(ang) - b * np.sin(ang), a * np.sin(ang) + b * np.cos(ang)],
+                           atol=2e-5)
+
+
+def _attn(heads, kv, hd, rot, L, rng, keys=None, values=None, qg=None, k=None, v=None):
+    ctx = L
+    qn, kn = np.ones(hd, np.float32), np.ones(hd, np.float32)
+    if keys is None:
+        keys = np.zeros((ctx, kv * hd), np.float32)
+        values = np.zeros((ctx, kv * hd), np.float32)
+        keys[:L - 1] = rng.standard_normal((L - 1, kv * hd))
+        values[:L - 1] = rng.standard_normal((L - 1, kv * hd))
+    qg = rng.standard_normal(heads * hd * 2).astype(np.float32) if qg is None else qg
+    k = rng.standard_normal(kv * hd).astype(np.float32) if k is None else k
+    v = rng.standard_normal(kv * hd).astype(np.float32) if v is None else v
+    out = oracle.attention(heads, kv, hd, rot, 1e7, 1e-6, qn, kn, qg, k, v, keys, values, L, L - 1)
+    return out, keys, values, qg, k, v
+
+
+def _sig(x):
+    return 1 / (1 + np.exp(-x.astype(np.float64)))
+
+
+def test_attention_single_position_is_gated_value():
+    """L = 1: softmax over one key is 1, so o = v[kv head] * sigmoid(gate)."""
+    rng = np.random.default_rng(1)
+    heads, kv, hd = 4, 2, 64
+    out, keys, values, qg, k, v = _attn(heads, kv, hd, 16, 1, rng)
+    for h in range(heads):
+        kh = h // (heads // kv)
+        gate = qg[h * hd * 2 + hd:(h + 1) * hd * 2]
+        assert np.allclose(out[h * hd:(h + 1) * hd], v[kh * hd:(kh + 1) * hd] * _sig(gate), rtol=1e-5, atol=1e-6)
+    # the new key was normalised and stored (RoPE at pos 0 is the identity)
+    kh0 = k[:hd] / np.sqrt(np.mean(k[:hd].astype(np.float64) ** 2) + 1e-6)
+    assert np.allclose(keys[0, :hd], kh0, rtol=1e-5)
+
+
+def test_attention_equal_keys_average_values():
+    """Identical keys give uniform weights: o = mean of v over positions (GQA head map)."""
+    rng = np.random.default_rng(2)
+    heads, kv, hd, L = 4, 2, 64, 9
+    base = rng.standard_normal(kv * hd).astype(np.float32)
+    keys = np.zeros((L, kv * hd), np.float32)
+    values = rng.standard_normal((L, kv * hd)).astype(np.float32)
+    # the stored keys are post-norm; the new one is normalised with unit weights, so store
+    # the normalised version of `base` at every earlier position (RoPE differs by position,
+    # so use rotary = 0 to keep every key identical)
+    kn = np.concatenate([base[i * hd:(i + 1) * hd] / np.sqrt(np.mean(base[i * hd:(i + 1) * hd].astype(np.float64) ** 2) + 1e-6)
+                         for i in range(kv)]).astype(np.float32)
+    keys[:L - 1] = kn
+    v_new = values[L - 1].copy()
+    qg = rng.standard_normal(heads * hd * 2).astype(np.float32)
+    out = oracle.attention(heads, kv, hd, 0, 1e7, 1e-6, np.ones(hd, np.float32), np.ones(hd, np.float32), qg, base,
+                           v_new, keys, values, L, L - 1)
+    for h in range(heads):
+        kh = h // (heads // kv)
+        gate = qg[h * hd * 2 + hd:(h + 1) * hd * 2]
+        want = values[:, kh * hd:(kh + 1) * hd].astype(np.float64).mean(0) * _sig(gate)
+        assert np.allclose(out[h * hd:(h + 1) * hd], want, rtol=1e-4, atol=1e-5)
+
+
+def test_attention_float64_brute_force():
+    rng = np.random.default_rng(3)
+    heads, kv, hd, rot, L = 8, 2, 64, 16, 40
+    out, keys, values, qg, k, v = _attn(heads, kv, hd, rot, L, rng)
+    pos = L - 1
+    for h in range(heads):
+        kh = h // (heads // kv)
+        q = qg[h * hd * 2:h * hd * 2 + hd].astype(np.float64)
+        q = q / np.sqrt(np.mean(q ** 2) + 1e-6)
+        half = rot // 2
+        ang = pos / np.power(1e7, 2 * np.arange(half) / rot)
+        a, b = q[:half].copy(), q[half:rot].copy()
+        q[:half], q[half:rot] = a * np.cos(ang) - b * np.sin(ang), a * np.sin(ang) + b * np.cos(ang)
+        K = keys[:L, kh * hd:(kh + 1) * hd].astype(np.float64)
+        V = values[:L, kh * hd:(kh + 1) * hd].astype(np.float64)
+        s = K @ q / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        want = (p / p.sum()) @ V * _sig(qg[h * hd * 2 + hd:(h + 1) * hd * 2])
+        assert np.allclose(out[h * hd:(h + 1) * hd], want, rtol=1e-4, atol=1e-5)
+
+
+def _dn(kh, vh, sd, cw, qkv, gate, alpha, beta, conv, a, dt, nw, cs, rs):
+    return oracle.delta_net(kh, vh, sd, cw, 1e-6, qkv, gate, alpha, beta, conv, a, dt, nw, cs, rs)
+
+
+def test_delta_net_zero_state_closed_form():
+    """Zero state: S = b * v k^T, so o_d = b v_d (k.q) before the norm/gate; with
+    beta -> -inf (b = 0) the state stays zero and the output is zero."""
+    rng = np.random.default_rng(4)
+    kh, vh, sd, cw = 1, 2, 64, 4
+    ch = 2 * kh * sd + vh * sd
+    conv = np.zeros(ch * cw, np.float32)
+    conv[cw - 1::cw] = 1.0  # taps pick the newest input: conv output = silu(x)
+    qkv = rng.standard_normal(ch).astype(np.float32)
+    gate = np.full(vh * sd, 30.0, np.float32)  # silu(30) = 30 (sigmoid ~ 1)
+    a = np.full(vh, -1.0, np.float32)
+    dt = np.zeros(vh, np.float32)
+    nw = np.ones(sd, np.float32)
+    alpha = np.zeros(vh, np.float32)
+    beta = np.array([40.0, -40.0], np.float32)  # b = 1 for head 0, b ~ 0 for head 1
+    cs, rs = np.zeros(ch * cw, np.float32), np.zeros(vh * sd * sd, np.float32)
+    out = _dn(kh, vh, sd, cw, qkv, gate, alpha, beta, conv, a, dt, nw, cs, rs)
+    silu = lambda x: x / (1 + np.exp(-x.astype(np.float64)))
+    c = silu(qkv)
+    q, k, v = c[:sd], c[sd:2 * sd], c[2 * sd:]
+    qh = q / np.sqrt((q ** 2).sum() + 1e-6) / np.sqrt(sd)
+    kn = k / np.sqrt((k ** 2).sum() + 1e-6)
+    o0 = v[:sd] * (kn @ qh)
+    o0 = o0 / np.sqrt(np.mean(o0 ** 2) + 1e-6) * 30.0
+    assert np.allclose(out[:sd], o0, rtol=2e-4, atol=1e-5)
+    S0 = np.outer(v[:sd], kn)
+    assert np.allclose(rs[:sd * sd].reshape(sd, sd), S0, rtol=1e-5, atol=1e-6)
+    assert np.max(np.abs(rs[sd * sd:])) < 1e-15 * 0 + 1e-16
+
+
+def test_delta_net_decay_only_when_beta_closed():
+    """b = 0: the state is only multiplied by decay = exp(a * softplus(alpha + dt))."""
+    rng = np.random.default_rng(5)
+    kh, vh, sd, cw = 1, 1, 64, 4
+    ch = 2 * kh * sd + vh * sd
+    rs = rng.standard_normal(sd * sd).astype(np.float32)
+    before = rs.copy()
+    cs = np.zeros(ch * cw, np.float32)
+    a, dt, alpha = np.array([-0.7], np.float32), np.array([0.3], np.float32), np.array([0.2], np.float32)
+    _dn(kh, vh, sd, cw, rng.standard_normal(ch).astype(np.float32), np.ones(sd, np.float32), alpha,
+        np.array([-200.0], np.float32), np.ones(ch * cw, np.float32), a, dt, np.ones(sd, np.float32), cs, rs)
+    decay = np.exp(-0.7 * np.log1p(np.exp(0.5)))
+    assert np.allclose(rs, before * decay, rtol=1e-6)
+
+
+def test_delta_net_conv_history_shifts():
+    """The conv state is the last conv_width inputs per channel, oldest first."""
+    kh, vh, sd, cw = 1, 1, 64, 3
+    ch = 2 * kh * sd + vh * sd
+    cs, rs = np.zeros(ch * cw, np.float32), np.zeros(sd * sd, np.float32)
+    ones = np.ones(ch * cw, np.float32)
+    for t in range(4):
+        qkv = np.full(ch, float(t + 1), np.float32)
+        _dn(kh, vh, sd, cw, qkv, np.ones(sd, np.float32), np.zeros(1, np.float32), np.zeros(1, np.float32), ones,
+            np.full(1, -1.0, np.float32), np.zeros(1, np.float32), np.ones(sd, np.float32), cs, rs)
+    assert np.array_equal(cs.reshape(ch, cw)[0], [2.0, 3.0, 4.0])
