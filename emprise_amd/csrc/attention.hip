@@ -7,8 +7,9 @@
 // its query heads and of the new key (a few KiB of work); the workgroup whose chunk
 // holds the current position also appends the new k/v to the caches and uses them
 // straight from LDS. Each workgroup writes an unnormalised partial (o, running max,
-// sum of exponentials); the last workgroup of a KV head to finish (an atomic ticket)
-// merges the partials, divides, and applies the sigmoid output gate.
+// sum of exponentials); a second small kernel merges the partials, divides, and applies
+// the sigmoid output gate. (A last-workgroup merge inside the first kernel would need
+// device-scope fences, which write back and invalidate a whole L2 on this part.)
 //
 // The grid covers the whole context so the launch can be replayed from a hipGraph:
 // the position is read from device memory and chunks past it return at once.
@@ -29,7 +30,6 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     __shared__ float sc[kMaxGroup][CH];
     __shared__ float acc_lds[kAttnWaves][kMaxGroup][HD];
     __shared__ float mstat[kMaxGroup], lstat[kMaxGroup];
-    __shared__ unsigned int ticket;
 
     const int group = a.heads / a.kv_heads;
     const int chunks_max = (a.context + CH - 1) / CH;
@@ -152,30 +152,33 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         part[threadIdx.x * stride + HD] = mstat[threadIdx.x];
         part[threadIdx.x * stride + HD + 1] = lstat[threadIdx.x];
     }
-    // the last chunk of this KV head to finish merges all partials
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) ticket = atomicAdd(&a.counter[kvh], 1u);
-    __syncthreads();
-    if (ticket != (unsigned)(nchunks - 1)) return;
-    __threadfence();
-    const float* base = a.partial + (size_t)kvh * chunks_max * group * stride;
-    for (int idx = threadIdx.x; idx < group * HD; idx += blockDim.x) {
-        const int g = idx / HD, d = idx % HD;
-        float M = -INFINITY;
-        for (int c = 0; c < nchunks; ++c) M = fmaxf(M, base[((size_t)c * group + g) * stride + HD]);
-        float num = 0.f, den = 0.f;
-        for (int c = 0; c < nchunks; ++c) {
-            const float* p = base + ((size_t)c * group + g) * stride;
-            const float wgt = expf(p[HD] - M);
-            num = fmaf(wgt, p[d], num);
-            den = fmaf(wgt, p[HD + 1], den);
-        }
-        const int head = kvh * group + g;
-        const float gate = a.qkv[(size_t)head * HD * 2 + HD + d];
-        a.out[(size_t)head * HD + d] = (num / den) * sigmoidf_(gate);
+}
+
+// Merges the chunk partials of every query head: o = sum_c e^(m_c - M) o_c /
+// sum_c e^(m_c - M) l_c, then the sigmoid output gate (model.cpp:153). One thread per
+// output value; the grid covers heads * head_dim.
+__global__ void attention_combine_kernel(AttnArgs a) {
+    const int hd = a.head_dim, group = a.heads / a.kv_heads;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= a.heads * hd) return;
+    const int pos = *a.position;
+    if (pos < 0 || pos >= a.context) return;
+    const int head = idx / hd, d = idx % hd, kvh = head / group, g = head % group;
+    const int chunks_max = (a.context + kAttnChunk - 1) / kAttnChunk;
+    const int nchunks = (pos + kAttnChunk) / kAttnChunk;
+    const int stride = hd + 2;
+    const float* base = a.partial + (size_t)kvh * chunks_max * group * stride + (size_t)g * stride;
+    float M = -INFINITY;
+    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, base[(size_t)c * group * stride + hd]);
+    float num = 0.f, den = 0.f;
+    for (int c = 0; c < nchunks; ++c) {
+        const float* p = base + (size_t)c * group * stride;
+        const float wgt = expf(p[hd] - M);
+        num = fmaf(wgt, p[d], num);
+        den = fmaf(wgt, p[hd + 1], den);
     }
-    if (threadIdx.x == 0) a.counter[kvh] = 0u;
+    const float gate = a.qkv[(size_t)head * hd * 2 + hd + d];
+    a.out[(size_t)head * hd + d] = (num / den) * sigmoidf_(gate);
 }
 
 }  // namespace
@@ -196,6 +199,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
     case 256: hipLaunchKernelGGL(attention_kernel<4>, grid, block, 0, stream, a); break;
     default: return hipErrorInvalidValue;
     }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3((a.heads * a.head_dim + 255) / 256), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

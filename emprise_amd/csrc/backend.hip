@@ -190,9 +190,13 @@ emprise_status run_matvec(emprise_hip* h, const Proj* p, int n, int mode, const 
         a.cols = (int)cols;
         a.mode = mode;
         int g = 0;
+        uint64_t total_rows = 0;
+        for (int s = 0; s < a.nseg; ++s)
+            if (!(mode == kMvSwiglu && s == 1)) total_rows += p[i + s].w->rows;
+        const int R = matvec_rows_per_group(type, cols, mode, total_rows);
+        a.rows_per_group = R;
         for (int s = 0; s < a.nseg; ++s) {
             const Weight* w = p[i + s].w;
-            const int R = (type == kQ6K || type == kQ4K) ? kMvRows : 1;
             a.seg[s].w = w->dev;
             a.seg[s].y = p[i + s].y;
             a.seg[s].rows = (int)w->rows;
@@ -364,12 +368,9 @@ emprise_status emprise_hip_upload_weight(emprise_hip* h, uint32_t type, uint64_t
         for (uint64_t r0 = 0; r0 < rows && err == hipSuccess; r0 += slab_rows) {
             const uint64_t n = std::min(slab_rows, rows - r0);
             parallel_rows(n, [&](uint64_t b, uint64_t e) {
-                for (uint64_t r = b; r < e; ++r) {
-                    const uint8_t* s = src + (r0 + r) * row_bytes;
-                    uint8_t* d = buf.data() + r * row_bytes;
-                    if (type == kQ6K) q6_row_to_device(s, d, nb);
-                    else q4_row_to_device(s, d, nb);
-                }
+                std::vector<uint8_t> tmp(row_bytes);
+                for (uint64_t r = b; r < e; ++r)
+                    row_to_device(type, src + (r0 + r) * row_bytes, buf.data() + r * row_bytes, cols, tmp.data());
             });
             err = hipMemcpy(w.dev + r0 * row_bytes, buf.data(), (size_t)(n * row_bytes), hipMemcpyHostToDevice);
         }
@@ -422,10 +423,9 @@ emprise_status emprise_hip_weight_download_gguf(emprise_hip* h, emprise_weight i
         const uint64_t nb = w->cols / 256, row_bytes = nb * type_block_bytes(w->type);
         auto* dst = static_cast<uint8_t*>(out);
         parallel_rows(w->rows, [&](uint64_t b, uint64_t e) {
-            for (uint64_t r = b; r < e; ++r) {
-                if (w->type == kQ6K) q6_row_from_device(buf.data() + r * row_bytes, dst + r * row_bytes, nb);
-                else q4_row_from_device(buf.data() + r * row_bytes, dst + r * row_bytes, nb);
-            }
+            std::vector<uint8_t> tmp(row_bytes);
+            for (uint64_t r = b; r < e; ++r)
+                row_from_device(w->type, buf.data() + r * row_bytes, dst + r * row_bytes, w->cols, tmp.data());
         });
     } else {
         std::memcpy(out, buf.data(), w->bytes);
@@ -636,11 +636,8 @@ emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention
         qn->rows * qn->cols != (uint64_t)p->head_dim || kn->rows * kn->cols != (uint64_t)p->head_dim)
         return fail(EMPRISE_EINVAL, "Attention projection dimensions");
     void* partial;
-    void* counter;
     TRY(h->get_scratch("attn_partial", attention_partial_floats(p->heads, p->kv_heads, p->head_dim, p->context) * sizeof(float),
                        &partial));
-    TRY(h->get_scratch("attn_counter", 64 * sizeof(unsigned), &counter, true));
-    if (p->kv_heads > 64) return fail(EMPRISE_EINVAL, "too many KV heads");
     AttnArgs a{};
     a.heads = p->heads;
     a.kv_heads = p->kv_heads;
@@ -657,7 +654,6 @@ emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention
     a.position = reinterpret_cast<const int*>(p->position);
     a.out = reinterpret_cast<float*>(out);
     a.partial = static_cast<float*>(partial);
-    a.counter = static_cast<unsigned*>(counter);
     return traced(h, "attention", 0, [&] { return launch_attention(a, h->stream); });
 }
 

@@ -21,6 +21,33 @@ __device__ __forceinline__ void q4_scale_min(const uint8_t* s, int j, int& sc, i
 // (d*sc)*q - dmin*m are formed in the same order.
 __device__ __forceinline__ float decode_element(const uint8_t* w, uint32_t type, int cols, uint64_t r, int k) {
     const int nb = cols / 256;
+    if (type == kQ6K && cols % kChunkCols == 0) {
+        const uint8_t* ch = w + r * (uint64_t)nb * 210 + (size_t)(k / kChunkCols) * 3360;
+        const int kk = k % kChunkCols, u = kk >> 4, t = kk & 15;
+        int code;
+        if (t < 12) {
+            code = ch[(t >> 2) * 1024 + 4 * u + (t & 3)] & 63;
+        } else {
+            const int b = t - 12;
+            code = (ch[4 * u + b] >> 6) | ((ch[1024 + 4 * u + b] >> 6) << 2) | ((ch[2048 + 4 * u + b] >> 6) << 4);
+        }
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(ch + 3328 + 2 * (u >> 4)));
+        const float sc = (float)(int8_t)ch[3072 + u];
+        return d * sc * (float)(code - 32);
+    }
+    if (type == kQ4K && cols % kChunkCols == 0) {
+        const uint8_t* ch = w + r * (uint64_t)nb * 144 + (size_t)(k / kChunkCols) * 2304;
+        const int kk = k % kChunkCols, u = kk >> 5, t = kk & 31;
+        const uint8_t byte = ch[(u & 1) * 1024 + 16 * (u >> 1) + 4 * ((t & 15) >> 2) + (t & 3)];
+        const int code = t < 16 ? (byte & 15) : (byte >> 4);
+        const uint8_t* s = ch + 2048 + 12 * (u >> 3);
+        const int j = u & 7;
+        const int sc = s[j] & 63, mn = ((s[j] >> 6) << 4) | ((s[8 + (j >> 1)] >> (4 * (j & 1))) & 15);
+        const uint8_t* dp = ch + 2240 + 4 * (u >> 3);
+        const float dd = half_bits_to_float(*reinterpret_cast<const uint16_t*>(dp));
+        const float dm = half_bits_to_float(*reinterpret_cast<const uint16_t*>(dp + 2));
+        return (dd * (float)sc) * (float)code - dm * (float)mn;
+    }
     if (type == kQ6K) {
         const uint8_t* row = w + r * (uint64_t)nb * 210;
         const int u = k >> 4, t = k & 15;

@@ -7,7 +7,9 @@
 namespace emprise {
 
 constexpr int kMaxSeg = 8;
-constexpr int kMvRows = 2;  // rows per wave iteration
+constexpr int kMvRows = 2;            // rows per wave iteration (unit-major rows)
+constexpr int kMvStreamRows = 2;      // rows per item of the streaming kernel (chunked rows)
+constexpr int kMvStreamPairRows = 2;  // gate/up row pairs per item of the SwiGLU variant
 
 enum MvMode : int { kMvPlain = 0, kMvSwiglu = 1, kMvArgmax = 2 };
 
@@ -37,10 +39,15 @@ struct MvArgs {
     const float* conv_w;  // [rows][conv_width]
     float* conv_state;    // [rows][conv_width]
     int conv_width;
+    int rows_per_group;   // R of the launch (matvec_rows_per_group)
 };
 
 size_t matvec_lds_bytes(uint32_t type, int cols, bool q8);
+// rows each row-group of MvArgs covers for this weight shape, mode and the launch's
+// total output rows (small launches use one row per wave to spread their arithmetic)
+int matvec_rows_per_group(uint32_t type, uint64_t cols, int mode, uint64_t total_rows);
 hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, hipStream_t stream);
+hipError_t launch_matvec_stream(uint32_t type, bool q8, const MvArgs& a, hipStream_t stream);
 hipError_t launch_dequant_rows(const uint8_t* w, uint32_t type, int cols, uint64_t row0, uint64_t n, float* out,
                                hipStream_t stream);
 
@@ -74,8 +81,7 @@ struct AttnArgs {
     float* values;
     const int* position;
     float* out;
-    float* partial;         // scratch: [kv_heads][chunks][group][head_dim + 2]
-    unsigned int* counter;  // scratch: [kv_heads], zero between launches
+    float* partial;  // scratch: [kv_heads][chunks][group][head_dim + 2]
 };
 constexpr int kAttnChunk = 64;
 size_t attention_partial_floats(int heads, int kv_heads, int head_dim, int context);

@@ -78,39 +78,6 @@ __device__ void stage_q8(int n, const float* xs, int8_t* xq, float* xscale, int*
     }
 }
 
-// The same quantisation with eight values per thread: the four threads of a 32-value
-// block combine their maxima with xor-shuffles inside a quad, then each rounds its own
-// eight values. Requires n % 2048 == 0 so every lane of the block has work.
-__device__ void stage_q8_wide(int n, const float* xs, int8_t* xq, float* xscale, int* qsum) {
-    for (int e = threadIdx.x; e < n / 8; e += blockDim.x) {
-        const float4 v0 = reinterpret_cast<const float4*>(xs)[2 * e];
-        const float4 v1 = reinterpret_cast<const float4*>(xs)[2 * e + 1];
-        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        float amax = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        const float s = amax / 127.f;
-        int q[8], part = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            q[i] = s != 0.f ? (int)roundf(v[i] / s) : 0;
-            part += q[i];
-        }
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lo |= (uint32_t)(q[i] & 0xff) << (8 * i);
-            hi |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
-        }
-        reinterpret_cast<uint2*>(xq)[e] = make_uint2(lo, hi);
-        part += __shfl_xor(part, 1, 64);  // the two threads of one 16-value unit
-        if ((e & 1) == 0) qsum[e >> 1] = part;
-        if ((e & 3) == 0) xscale[e >> 2] = half_bits_to_float(float_to_half_bits(s));
-    }
-}
-
 // ---- per-unit dot products --------------------------------------------------------
 
 __device__ __forceinline__ float dot4(uint32_t q, const float4& x, float acc) {
@@ -312,157 +279,152 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
     }
 }
 
-// ---- streaming kernel for inputs that are a multiple of 4096 wide ------------------------
+// ---- streaming kernel for rows in the chunked layout (cols % 4096 == 0) --------------
 //
-// Same lane -> unit mapping as above, but each wave walks a sequence of (row group,
-// 4096-column chunk) items and keeps the next item's weights in flight while it computes
-// the current one: the loads of item i+1 are issued before the arithmetic of item i,
-// and the very first item's loads are issued before the workgroup stages its input.
-// A chunk holds 64 weights per lane per row: 4 Q6_K units (12 B codes + scale + d each)
-// or 2 Q4_K units (16 B nibbles + 3 scale bytes + d/dmin each).
+// A wave walks a sequence of items (a group of R rows x one 4096-column chunk) and
+// keeps the next item's weights in flight while it computes the current one; the
+// first item's loads go out before the workgroup stages its input. Lane l owns 64
+// consecutive weights of every chunk row: per row and chunk it issues three (Q6_K) or
+// two (Q4_K) 16-byte loads that each cover 1 KiB contiguous across the wave, plus one
+// scale load and one d load. Row pointers are wave-uniform (scalar registers).
 
-template <int T, int NA> struct Chunk;
-template <int NA> struct Chunk<kQ6K, NA> {
-    uint32_t q[NA][4][3];
-    int32_t sc[NA][4];
-    uint32_t d[NA][4];
+// LDS slot of input float4 e in the streaming kernels: lane l's 16 float4 of chunk c
+// sit at (c*16 + i)*64 + l, so a wave reading float4 i of its lanes touches 1 KiB of
+// consecutive bytes (no bank conflicts).
+__device__ __forceinline__ int chunk_slot(int e) { return (((e >> 10) << 4) + (e & 15)) * 64 + ((e & 1023) >> 4); }
+
+template <int T, int NA> struct SChunk;
+template <int NA> struct SChunk<kQ6K, NA> {
+    uint4 q[NA][3];    // plane p: D_p of the lane's units 4l..4l+3
+    uint32_t sc[NA];   // the four int8 scales
+    uint32_t d[NA];    // fp16 d of the block
 };
-template <int NA> struct Chunk<kQ4K, NA> {
-    uint4 q[NA][2];
-    uint32_t b0[NA][2], b1[NA][2], b2[NA][2];  // scale bytes A, B, C (see q4_lane_scale)
-    uint32_t dd[NA][2];                        // fp16 d | fp16 dmin << 16
+template <int NA> struct SChunk<kQ4K, NA> {
+    uint4 q[NA][2];    // units 2l and 2l+1
+    uint32_t s2[NA];   // bytes j0, j0+1 of the re-packed scales (sc | m_hi << 6)
+    uint32_t m4[NA];   // m low nibbles of sub-blocks j0 (low) and j0+1 (high)
+    uint32_t dd[NA];   // fp16 d | fp16 dmin << 16
 };
 
-// Q4_K scale/min of sub-block j from three bytes: for j < 4, A = s[j], B = s[j+4];
-// for j >= 4, A = s[j+4], B = s[j-4], C = s[j] (quant.cpp:48-52).
-__device__ __forceinline__ void q4_offsets(int j, int& oa, int& ob, int& oc) {
-    oa = j < 4 ? j : j + 4;
-    ob = j < 4 ? j + 4 : j - 4;
-    oc = j;
+// Weight bytes are read once per token: non-temporal loads stream them past the caches.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 nt_u4(const uint8_t* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ void q4_lane_scale(int j, uint32_t A, uint32_t B, uint32_t C, int& sc, int& mn) {
-    if (j < 4) {
-        sc = A & 63;
-        mn = B & 63;
-    } else {
-        sc = (A & 15) | ((B >> 6) << 4);
-        mn = (A >> 4) | ((C >> 6) << 4);
-    }
+__device__ __forceinline__ uint32_t nt_u32(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
+__device__ __forceinline__ uint32_t nt_u16(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+}
+__device__ __forceinline__ uint32_t nt_u8(const uint8_t* p) { return __builtin_nontemporal_load(p); }
 
 template <int T, int NA>
-__device__ __forceinline__ void load_chunk(Chunk<T, NA>& ch, const uint8_t* const* rp, int nb, int c, int lane) {
+__device__ __forceinline__ void sload(SChunk<T, NA>& ch, const uint8_t* const* rp, int c, int lane) {
     if constexpr (T == kQ6K) {
-#pragma unroll
-        for (int r = 0; r < NA; ++r)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int u = c * 256 + lane + 64 * k;
-                const uint8_t* q = rp[r] + (size_t)u * 12;
-                ch.q[r][k][0] = ld_u32(q);
-                ch.q[r][k][1] = ld_u32(q + 4);
-                ch.q[r][k][2] = ld_u32(q + 8);
-                ch.sc[r][k] = (int8_t)rp[r][(size_t)nb * 192 + u];
-                ch.d[r][k] = *reinterpret_cast<const uint16_t*>(rp[r] + (size_t)nb * 208 + 2 * (u >> 4));
-            }
-    } else {
-        int oa, ob, oc;
-        q4_offsets(lane & 7, oa, ob, oc);
-#pragma unroll
-        for (int r = 0; r < NA; ++r)
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int u = c * 128 + lane + 64 * k;
-                ch.q[r][k] = *reinterpret_cast<const uint4*>(rp[r] + (size_t)u * 16);
-                const uint8_t* s = rp[r] + (size_t)nb * 128 + (size_t)(u >> 3) * 12;
-                ch.b0[r][k] = s[oa];
-                ch.b1[r][k] = s[ob];
-                ch.b2[r][k] = s[oc];
-                ch.dd[r][k] = *reinterpret_cast<const uint32_t*>(rp[r] + (size_t)nb * 140 + (size_t)(u >> 3) * 4);
-            }
-    }
-}
-
-template <int T, int NA>
-__device__ __forceinline__ void compute_chunk(const Chunk<T, NA>& ch, float* acc, const float* xs, const float* usum,
-                                              int c, int lane) {
-    if constexpr (T == kQ6K) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int u = c * 256 + lane + 64 * k;
-            float4 xv[4];
-            const float4* xp = reinterpret_cast<const float4*>(xs) + (size_t)((c * 4 + k) * 4) * 64 + lane;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) xv[i] = xp[i * 64];
-            const float xsum = usum[u];
-#pragma unroll
-            for (int r = 0; r < NA; ++r) {
-                const float s = q6_unit(ch.q[r][k][0], ch.q[r][k][1], ch.q[r][k][2], xv);
-                const float d = half_bits_to_float((uint16_t)ch.d[r][k]);
-                acc[r] = fmaf(d * (float)ch.sc[r][k], fmaf(-32.f, xsum, s), acc[r]);
-            }
-        }
-    } else {
-        const int j = lane & 7;
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int u = c * 128 + lane + 64 * k;
-            float4 xv[8];
-            const float4* xp = reinterpret_cast<const float4*>(xs) + (size_t)((c * 2 + k) * 8) * 64 + lane;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) xv[i] = xp[i * 64];
-            const float xsum = usum[u];
-#pragma unroll
-            for (int r = 0; r < NA; ++r) {
-                int sc, mn;
-                q4_lane_scale(j, ch.b0[r][k], ch.b1[r][k], ch.b2[r][k], sc, mn);
-                const float dd = half_bits_to_float((uint16_t)(ch.dd[r][k] & 0xffff));
-                const float dm = half_bits_to_float((uint16_t)(ch.dd[r][k] >> 16));
-                const float s = q4_unit(ch.q[r][k], xv);
-                acc[r] += (dd * (float)sc) * s - (dm * (float)mn) * xsum;
-            }
-        }
-    }
-}
-
-// Q8 activations (Q6_K only): integer dot of the codes with the int8 input per unit.
-template <int NA>
-__device__ __forceinline__ void compute_chunk_q8(const Chunk<kQ6K, NA>& ch, float* acc, const int8_t* xq,
-                                                 const float* xscale, const int* qsum, int c, int lane) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int u = c * 256 + lane + 64 * k;
-        const int4 xv = *reinterpret_cast<const int4*>(xq + (size_t)u * 16);
-        const int q32 = 32 * qsum[u];
-        const float s8 = xscale[u >> 1];
 #pragma unroll
         for (int r = 0; r < NA; ++r) {
-            const uint32_t d0 = ch.q[r][k][0], d1 = ch.q[r][k][1], d2 = ch.q[r][k][2];
+            const uint8_t* base = rp[r] + (size_t)c * 3360;
+#pragma unroll
+            for (int p = 0; p < 3; ++p) ch.q[r][p] = nt_u4(base + p * 1024 + 16 * lane);
+            ch.sc[r] = nt_u32(base + 3072 + 4 * lane);
+            ch.d[r] = nt_u16(base + 3328 + 2 * (lane >> 2));
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < NA; ++r) {
+            const uint8_t* base = rp[r] + (size_t)c * 2304;
+            ch.q[r][0] = nt_u4(base + 16 * lane);
+            ch.q[r][1] = nt_u4(base + 1024 + 16 * lane);
+            const uint8_t* s = base + 2048 + 12 * (lane >> 2);
+            ch.s2[r] = nt_u16(s + 2 * (lane & 3));
+            ch.m4[r] = nt_u8(s + 8 + (lane & 3));
+            ch.dd[r] = nt_u32(base + 2240 + 4 * (lane >> 2));
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t lane_word(const uint4& v, int j) {
+    return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+}
+
+template <int T, int NA>
+__device__ __forceinline__ void scompute(const SChunk<T, NA>& ch, float* acc, const float* xs, const float* usum, int c,
+                                         int lane) {
+    const float4* x4 = reinterpret_cast<const float4*>(xs) + (size_t)c * 1024 + lane;
+    if constexpr (T == kQ6K) {
+        const float4 xsum = reinterpret_cast<const float4*>(usum)[c * 64 + lane];
+        const float xsv[4] = {xsum.x, xsum.y, xsum.z, xsum.w};
+        float dv[NA];
+#pragma unroll
+        for (int r = 0; r < NA; ++r) dv[r] = half_bits_to_float((uint16_t)ch.d[r]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float4 xv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[i] = x4[(j * 4 + i) * 64];
+            const float off = -32.f * xsv[j];
+#pragma unroll
+            for (int r = 0; r < NA; ++r) {
+                const float s = q6_unit(lane_word(ch.q[r][0], j), lane_word(ch.q[r][1], j), lane_word(ch.q[r][2], j), xv);
+                const float sc = (float)(int)(int8_t)(ch.sc[r] >> (8 * j));
+                acc[r] = fmaf(dv[r] * sc, s + off, acc[r]);
+            }
+        }
+    } else {
+        const float2 xsum = reinterpret_cast<const float2*>(usum)[c * 64 + lane];
+        const float xsv[2] = {xsum.x, xsum.y};
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            float4 xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = x4[(p * 8 + i) * 64];
+#pragma unroll
+            for (int r = 0; r < NA; ++r) {
+                const uint32_t b = (ch.s2[r] >> (8 * p)) & 0xff;
+                const int sc = b & 63;
+                const int mn = ((b >> 6) << 4) | ((ch.m4[r] >> (4 * p)) & 15);
+                const float dd = half_bits_to_float((uint16_t)(ch.dd[r] & 0xffff));
+                const float dm = half_bits_to_float((uint16_t)(ch.dd[r] >> 16));
+                const float s = q4_unit(ch.q[r][p], xv);
+                acc[r] += (dd * (float)sc) * s - (dm * (float)mn) * xsv[p];
+            }
+        }
+    }
+}
+
+// Q8 activations (Q6_K only): int8 input in LDS, unit granules of 16 B at
+// ((c*4 + j)*64 + l)*16 for unit 4l+j of chunk c.
+template <int NA>
+__device__ __forceinline__ void scompute_q8(const SChunk<kQ6K, NA>& ch, float* acc, const int8_t* xq,
+                                            const float* xscale, const int* qsum, int c, int lane) {
+    const int4 qs = reinterpret_cast<const int4*>(qsum)[c * 64 + lane];
+    const float2 s8 = reinterpret_cast<const float2*>(xscale)[c * 64 + lane];
+    const int qsv[4] = {qs.x, qs.y, qs.z, qs.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int4 xv = reinterpret_cast<const int4*>(xq)[(c * 4 + j) * 64 + lane];
+        const float s8j = j < 2 ? s8.x : s8.y;
+#pragma unroll
+        for (int r = 0; r < NA; ++r) {
+            const uint32_t d0 = lane_word(ch.q[r][0], j), d1 = lane_word(ch.q[r][1], j), d2 = lane_word(ch.q[r][2], j);
             const uint32_t e = ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u);
             int dot = __builtin_amdgcn_sdot4((int)(d0 & 0x3F3F3F3Fu), xv.x, 0, false);
             dot = __builtin_amdgcn_sdot4((int)(d1 & 0x3F3F3F3Fu), xv.y, dot, false);
             dot = __builtin_amdgcn_sdot4((int)(d2 & 0x3F3F3F3Fu), xv.z, dot, false);
             dot = __builtin_amdgcn_sdot4((int)e, xv.w, dot, false);
-            const float d = half_bits_to_float((uint16_t)ch.d[r][k]);
-            acc[r] += ((float)(dot - q32) * (d * (float)ch.sc[r][k])) * s8;
+            const float d = half_bits_to_float((uint16_t)ch.d[r]);
+            const float sc = (float)(int)(int8_t)(ch.sc[r] >> (8 * j));
+            acc[r] += ((float)(dot - 32 * qsv[j]) * (d * sc)) * s8j;
         }
     }
 }
 
-// LDS slot of input float4 i. Interleaved (PERM): the float4s of 64 consecutive units
-// are stored lane-major -- float4 j of unit u at ((u/64)*(unit/4) + j)*64 + u%64 -- so
-// when lane l reads unit base+l every lane hits the next 16 bytes (no bank conflicts).
-template <bool PERM, int UNIT> __device__ __forceinline__ int xslot(int i) {
-    if constexpr (!PERM) return i;
-    constexpr int U4 = UNIT / 4;
-    const int u = i / U4, j = i % U4;
-    return ((u >> 6) * U4 + j) * 64 + (u & 63);
-}
-
-// Input staging with 16-byte loads, four in flight per thread.
-template <bool PERM, int UNIT>
-__device__ void stage_input_wide(const MvArgs& a, float* xs, float* usum, float* red) {
-    constexpr int unit = UNIT;
+// Input staging for the streaming kernels: 16-byte loads, four in flight per thread;
+// FP32 input goes to chunk_slot order, per-unit sums in natural order.
+template <int UNIT, bool Q8>
+__device__ void sstage(const MvArgs& a, float* xs, float* usum, float* red) {
     const int n4 = a.cols / 4;
     const bool writer = a.x_out && blockIdx.x == 0;
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
@@ -490,7 +452,7 @@ __device__ void stage_input_wide(const MvArgs& a, float* xs, float* usum, float*
             const int i = i0 + k * blockDim.x;
             if (i < n4) {
                 if (writer) reinterpret_cast<float4*>(a.x_out)[i] = v[k];
-                xs4[xslot<PERM, UNIT>(i)] = v[k];
+                xs4[Q8 ? i : chunk_slot(i)] = v[k];
                 ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
             }
         }
@@ -508,7 +470,7 @@ __device__ void stage_input_wide(const MvArgs& a, float* xs, float* usum, float*
             for (int k = 0; k < 4; ++k) {
                 const int i = i0 + k * blockDim.x;
                 if (i < n4) {
-                    const int sl = xslot<PERM, UNIT>(i);
+                    const int sl = Q8 ? i : chunk_slot(i);
                     float4 v = xs4[sl];
                     v.x = v.x * (scale * w[k].x);
                     v.y = v.y * (scale * w[k].y);
@@ -520,14 +482,51 @@ __device__ void stage_input_wide(const MvArgs& a, float* xs, float* usum, float*
         }
     }
     __syncthreads();
-    const int units = a.cols / unit;
-    for (int u = threadIdx.x; u < units; u += blockDim.x) {
-        float s = 0.f;
-        for (int j = 0; j < unit / 4; ++j) {
-            const float4 v = xs4[xslot<PERM, UNIT>(u * (unit / 4) + j)];
-            s += (v.x + v.y) + (v.z + v.w);
+    if constexpr (!Q8) {
+        constexpr int U4 = UNIT / 4;
+        const int units = a.cols / UNIT;
+        for (int u = threadIdx.x; u < units; u += blockDim.x) {
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < U4; ++j) {
+                const float4 v = xs4[chunk_slot(u * U4 + j)];
+                s += (v.x + v.y) + (v.z + v.w);
+            }
+            usum[u] = s;
         }
-        usum[u] = s;
+    }
+}
+
+// Q8 quantisation of the staged input (natural order) into unit granules at
+// ((c*4 + j)*64 + l)*16 for unit u = c*256 + 4l + j; 8 values per thread.
+__device__ void sstage_q8(int n, const float* xs, int8_t* xq, float* xscale, int* qsum) {
+    for (int e = threadIdx.x; e < n / 8; e += blockDim.x) {
+        const float4 v0 = reinterpret_cast<const float4*>(xs)[2 * e];
+        const float4 v1 = reinterpret_cast<const float4*>(xs)[2 * e + 1];
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        const float s = amax / 127.f;
+        int q[8], part = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            q[i] = s != 0.f ? (int)roundf(v[i] / s) : 0;
+            part += q[i];
+        }
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo |= (uint32_t)(q[i] & 0xff) << (8 * i);
+            hi |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
+        }
+        const int u = e >> 1, c = u >> 8, w = u & 255;
+        reinterpret_cast<uint2*>(xq)[(((c * 4 + (w & 3)) * 64 + (w >> 2)) << 1) + (e & 1)] = make_uint2(lo, hi);
+        part += __shfl_xor(part, 1, 64);
+        if ((e & 1) == 0) qsum[u] = part;
+        if ((e & 3) == 0) xscale[e >> 2] = half_bits_to_float(float_to_half_bits(s));
     }
 }
 
@@ -545,13 +544,12 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
     float* xscale = reinterpret_cast<float*>(xq + a.cols);
     int* qsum = reinterpret_cast<int*>(xscale + a.cols / 32);
 
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nb = a.cols / 256;
-    const int cpr = a.cols / 4096;  // chunks per row
-    const size_t row_bytes = (size_t)nb * Fmt<T>::block;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cpr = a.cols / kChunkCols;
+    const size_t row_bytes = (size_t)(a.cols / 256) * Fmt<T>::block;
     const int stride = gridDim.x * 4;
 
-    // row pointers of group g (clamped to the segment's last row)
     auto rows_of = [&](int g, const uint8_t** rp, int& s, int& row0) {
         s = 0;
         while (s + 1 < a.nseg && g >= a.seg[s + 1].g0) ++s;
@@ -568,15 +566,15 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
     int g = blockIdx.x * 4 + wave, c = 0;
     const uint8_t* rp[NA];
     int seg = 0, row0 = 0;
-    Chunk<T, NA> cur, nxt;
+    SChunk<T, NA> cur, nxt;
     if (g < a.groups) {
         rows_of(g, rp, seg, row0);
-        load_chunk<T, NA>(cur, rp, nb, 0, lane);
+        sload<T, NA>(cur, rp, 0, lane);
     }
-    stage_input_wide<!Q8, UW>(a, xs, usum, red);
+    sstage<UW, Q8>(a, xs, usum, red);
     if constexpr (Q8) {
         __syncthreads();
-        stage_q8_wide(a.cols, xs, xq, xscale, qsum);
+        sstage_q8(a.cols, xs, xq, xscale, qsum);
     }
     if (a.mode == kMvArgmax && threadIdx.x == 0) block_best = 0ull;
     __syncthreads();
@@ -593,15 +591,14 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
         }
         const uint8_t* rpn[NA];
         int segn = seg, row0n = row0;
+#pragma unroll
+        for (int r = 0; r < NA; ++r) rpn[r] = rp[r];
         if (gn < a.groups) {
             if (gn != g) rows_of(gn, rpn, segn, row0n);
-            else
-#pragma unroll
-                for (int r = 0; r < NA; ++r) rpn[r] = rp[r];
-            load_chunk<T, NA>(nxt, rpn, nb, cn, lane);
+            sload<T, NA>(nxt, rpn, cn, lane);
         }
-        if constexpr (Q8) compute_chunk_q8<NA>(cur, acc, xq, xscale, qsum, c, lane);
-        else compute_chunk<T, NA>(cur, acc, xs, usum, c, lane);
+        if constexpr (Q8) scompute_q8<NA>(cur, acc, xq, xscale, qsum, c, lane);
+        else scompute<T, NA>(cur, acc, xs, usum, c, lane);
         if (c == cpr - 1) {
 #pragma unroll
             for (int r = 0; r < NA; ++r) acc[r] = wave_sum(acc[r]);
@@ -642,6 +639,77 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
         if (threadIdx.x == 0 && block_best) atomicMax(a.argmax, block_best);
     }
 }
+
+// Workgroups of a streaming launch: one full round of resident workgroups (occupancy x
+// CUs), so every wave keeps two items in flight and none waits for a second round.
+// EMPRISE_MV_WAVES_PER_CU (resident waves per CU to aim for) overrides it for sweeps.
+template <class K> int resident_blocks(K kernel, size_t lds) {
+    static int cached = 0;
+    if (!cached) {
+        int dev = 0, per_cu = 0;
+        hipDeviceProp_t prop;
+        (void)hipGetDevice(&dev);
+        (void)hipGetDeviceProperties(&prop, dev);
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), 256, lds);
+        const char* e = getenv("EMPRISE_MV_WAVES_PER_CU");
+        const int want = e ? atoi(e) / 4 : 0;
+        if (want > 0 && want < per_cu) per_cu = want;
+        cached = (per_cu > 0 ? per_cu : 1) * prop.multiProcessorCount;
+    }
+    return cached;
+}
+
+template <class K> hipError_t launch_stream(K kernel, const MvArgs& a, size_t lds, hipStream_t stream) {
+    int blocks = (a.groups + 3) / 4;
+    const int cap = resident_blocks(kernel, lds);
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), lds, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// Rows per item of the streaming kernel: 2 rows (2 gate/up pairs) -- measured against 1
+// and 4 on the 9B shapes; more rows amortise the input reads, fewer spread the work. EMPRISE_MV_ROWS (1, 2 or 4) overrides it
+// for launch-shape sweeps.
+int matvec_rows_per_group(uint32_t type, uint64_t cols, int mode, uint64_t total_rows) {
+    (void)total_rows;
+    if ((type == kQ6K || type == kQ4K) && cols % kChunkCols == 0) {
+        static const int forced = [] {
+            const char* e = getenv("EMPRISE_MV_ROWS");
+            const int v = e ? atoi(e) : 0;
+            return (v == 1 || v == 2 || v == 4) ? v : 0;
+        }();
+        if (mode == kMvSwiglu) return forced ? (forced > 2 ? 2 : forced) : kMvStreamPairRows;
+        return forced ? forced : kMvStreamRows;
+    }
+    return (type == kQ6K || type == kQ4K) ? kMvRows : 1;
+}
+
+template <int T, bool Q8, bool PAIR> static hipError_t launch_stream_r(const MvArgs& a, size_t lds, hipStream_t stream) {
+    switch (a.rows_per_group) {
+    case 1: return launch_stream(matvec_stream_kernel<T, 1, Q8, PAIR>, a, lds, stream);
+    case 2: return launch_stream(matvec_stream_kernel<T, 2, Q8, PAIR>, a, lds, stream);
+    case 4:
+        if constexpr (!PAIR) return launch_stream(matvec_stream_kernel<T, 4, Q8, PAIR>, a, lds, stream);
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_matvec_stream(uint32_t type, bool q8, const MvArgs& a, hipStream_t stream) {
+    const size_t lds = matvec_lds_bytes(type, a.cols, q8);
+    const bool pair = a.mode == kMvSwiglu;
+    if (type == kQ6K) {
+        if (q8) return pair ? launch_stream_r<kQ6K, true, true>(a, lds, stream) : launch_stream_r<kQ6K, true, false>(a, lds, stream);
+        return pair ? launch_stream_r<kQ6K, false, true>(a, lds, stream) : launch_stream_r<kQ6K, false, false>(a, lds, stream);
+    }
+    return pair ? launch_stream_r<kQ4K, false, true>(a, lds, stream) : launch_stream_r<kQ4K, false, false>(a, lds, stream);
+}
+
+namespace {
+
 
 // Plain-layout (F32 / F16 / BF16) matvec: one wave per row, lanes stride the columns.
 template <int T>
@@ -720,34 +788,6 @@ size_t matvec_lds_bytes(uint32_t type, int cols, bool q8) {
     return (size_t)cols * 4 + 16;
 }
 
-// Workgroups of a streaming launch: one full round of resident workgroups (occupancy x
-// CUs), so every wave keeps two items in flight and none waits for a second round.
-// EMPRISE_MV_WAVES_PER_CU (resident waves per CU to aim for) overrides it for sweeps.
-template <class K> static int resident_blocks(K kernel, size_t lds) {
-    static int cached = 0;
-    if (!cached) {
-        int dev = 0, per_cu = 0;
-        hipDeviceProp_t prop;
-        (void)hipGetDevice(&dev);
-        (void)hipGetDeviceProperties(&prop, dev);
-        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), 256, lds);
-        const char* e = getenv("EMPRISE_MV_WAVES_PER_CU");
-        const int want = e ? atoi(e) / 4 : 0;
-        if (want > 0 && want < per_cu) per_cu = want;
-        cached = (per_cu > 0 ? per_cu : 1) * prop.multiProcessorCount;
-    }
-    return cached;
-}
-
-template <class K> static hipError_t launch_stream(K kernel, const MvArgs& a, size_t lds, hipStream_t stream) {
-    int blocks = (a.groups + 3) / 4;
-    const int cap = resident_blocks(kernel, lds);
-    if (blocks > cap) blocks = cap;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), lds, stream, a);
-    return hipGetLastError();
-}
-
 hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, hipStream_t stream) {
     const size_t lds = matvec_lds_bytes(type, a.cols, q8);
     int blocks = (a.groups + 3) / 4;
@@ -755,16 +795,7 @@ hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, 
     if (blocks < 1) blocks = 1;
     const dim3 grid(blocks), block(256);
     const bool pair = a.mode == kMvSwiglu;
-    if ((type == kQ6K || type == kQ4K) && a.cols % 4096 == 0) {
-        if (type == kQ6K) {
-            if (q8) return pair ? launch_stream(matvec_stream_kernel<kQ6K, kMvRows, true, true>, a, lds, stream)
-                                : launch_stream(matvec_stream_kernel<kQ6K, kMvRows, true, false>, a, lds, stream);
-            return pair ? launch_stream(matvec_stream_kernel<kQ6K, kMvRows, false, true>, a, lds, stream)
-                        : launch_stream(matvec_stream_kernel<kQ6K, kMvRows, false, false>, a, lds, stream);
-        }
-        return pair ? launch_stream(matvec_stream_kernel<kQ4K, kMvRows, false, true>, a, lds, stream)
-                    : launch_stream(matvec_stream_kernel<kQ4K, kMvRows, false, false>, a, lds, stream);
-    }
+    if ((type == kQ6K || type == kQ4K) && a.cols % kChunkCols == 0) return launch_matvec_stream(type, q8, a, stream);
     switch (type) {
     case kQ6K:
         if (q8) {
