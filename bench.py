@@ -105,6 +105,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--trace-steps", type=int, default=3)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch every kernel from the host instead of replaying the step graph (for profilers)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU decode is not part of "
@@ -114,7 +116,7 @@ def main():
     import emprise_amd as ea
     path = model_file(args.model, seed=0)
     t = time.time()
-    model = ea.Model(path, context=args.context, fast_q8=args.fast_q8)
+    model = ea.Model(path, context=args.context, fast_q8=args.fast_q8, graph=not args.no_graph)
     info = model.info
     log(f"loaded {path.name}: {info.weight_bytes / 1e9:.3f} GB on device in {time.time() - t:.1f}s "
         f"({model.backend_name}); {info.token_weight_bytes / 1e9:.4f} GB streamed per token")

@@ -44,6 +44,27 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     const float* kin = a.qkv + qd + (size_t)kvh * HD;
     const float* vin = a.qkv + qd + kvd + (size_t)kvh * HD;
 
+    // Wave w owns positions t0 + w, t0 + w + 4, ...: all of its K and V rows are loaded
+    // here, before any arithmetic, so their latency overlaps the norms and RoPE below.
+    // (The row at `pos` is not written yet; its value is replaced by the new k/v.)
+    constexpr int PW = CH / kAttnWaves;
+    const int t0 = chunk * CH;
+    const int tn = min(CH, len - t0);
+    const size_t row_stride = (size_t)a.kv_heads * HD;
+    const float* kb = a.keys + ((size_t)t0 * a.kv_heads + kvh) * HD + lane;
+    const float* vb = a.values + ((size_t)t0 * a.kv_heads + kvh) * HD + lane;
+    float kr[PW][E], vr[PW][E];
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+        const int tt = wave + kAttnWaves * i;
+        if (tt < tn) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) kr[i][e] = kb[(size_t)tt * row_stride + 64 * e];
+#pragma unroll
+            for (int e = 0; e < E; ++e) vr[i][e] = vb[(size_t)tt * row_stride + 64 * e];
+        }
+    }
+
     // RMSNorm of the query heads (wave g handles heads g, g+4, ...) and of the new key.
     for (int g = wave; g <= group; g += kAttnWaves) {
         const float* src = g < group ? a.qkv + (size_t)(kvh * group + g) * HD * 2 : kin;
@@ -74,8 +95,6 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         row[i + half] = x0 * s + x1 * c;
     }
     __syncthreads();
-    const int t0 = chunk * CH;
-    const int tn = min(CH, len - t0);
     if (chunk == nchunks - 1) {  // this chunk holds `pos`: append k/v to the caches
         for (int d = threadIdx.x; d < HD; d += blockDim.x) {
             a.keys[((size_t)pos * a.kv_heads + kvh) * HD + d] = knew[d];
@@ -83,20 +102,22 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         }
     }
 
-    // scores s[g][t] = q_g . k_t / sqrt(HD)
+    // scores s[g][t] = q_g . k_t / sqrt(HD); the wave's K rows were loaded up front
     const float inv_root = 1.f / sqrtf((float)HD);
-    for (int tt = wave; tt < tn; tt += kAttnWaves) {
-        const int t = t0 + tt;
-        float kr[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e)
-            kr[e] = t == pos ? knew[lane + 64 * e] : a.keys[((size_t)t * a.kv_heads + kvh) * HD + lane + 64 * e];
-        for (int g = 0; g < group; ++g) {
-            float dot = 0.f;
+    for (int i = 0; i < PW; ++i) {
+        const int tt = wave + kAttnWaves * i;
+        if (tt < tn) {
+            if (t0 + tt == pos)
 #pragma unroll
-            for (int e = 0; e < E; ++e) dot += qs[g][lane + 64 * e] * kr[e];
-            dot = wave_sum(dot);
-            if (lane == 0) sc[g][tt] = dot * inv_root;
+                for (int e = 0; e < E; ++e) kr[i][e] = knew[lane + 64 * e];
+            for (int g = 0; g < group; ++g) {
+                float dot = 0.f;
+#pragma unroll
+                for (int e = 0; e < E; ++e) dot += qs[g][lane + 64 * e] * kr[i][e];
+                dot = wave_sum(dot);
+                if (lane == 0) sc[g][tt] = dot * inv_root;
+            }
         }
     }
     __syncthreads();
@@ -119,18 +140,20 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     for (int g = 0; g < kMaxGroup; ++g)
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
-    for (int tt = wave; tt < tn; tt += kAttnWaves) {
-        const int t = t0 + tt;
-        float vr[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e)
-            vr[e] = t == pos ? vnew[lane + 64 * e] : a.values[((size_t)t * a.kv_heads + kvh) * HD + lane + 64 * e];
+    for (int i = 0; i < PW; ++i) {
+        const int tt = wave + kAttnWaves * i;
+        if (tt < tn) {
+            if (t0 + tt == pos)
 #pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            if (g < group) {
-                const float p = sc[g][tt];
+                for (int e = 0; e < E; ++e) vr[i][e] = vnew[lane + 64 * e];
 #pragma unroll
-                for (int e = 0; e < E; ++e) acc[g][e] = fmaf(p, vr[e], acc[g][e]);
+            for (int g = 0; g < kMaxGroup; ++g) {
+                if (g < group) {
+                    const float p = sc[g][tt];
+#pragma unroll
+                    for (int e = 0; e < E; ++e) acc[g][e] = fmaf(p, vr[i][e], acc[g][e]);
+                }
             }
         }
     }

@@ -45,7 +45,9 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_kernel(GdnArgs a) {
     const float* v = a.qkv + 2 * (size_t)key_dim + (size_t)h * SD;
     float* S = a.state + (size_t)h * SD * SD;
 
-    // issue the state reads of this wave's rows first
+    // issue the state reads of this wave's rows first; lane r also fetches v of row r
+    // (read back with readlane, so no load waits behind the state stores of the loop)
+    const float v_lane = lane < RPW ? v[wave * RPW + lane] : 0.f;
     float s[RPW][E];
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
@@ -82,7 +84,8 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_kernel(GdnArgs a) {
             mem += s[r][e] * kv[e];
         }
         mem = wave_sum(mem);
-        const float delta = (v[d] - mem) * b;
+        const float vd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_lane), r));
+        const float delta = (vd - mem) * b;
         float sum = 0.f;
 #pragma unroll
         for (int e = 0; e < E; ++e) {

@@ -423,13 +423,63 @@ __device__ __forceinline__ void scompute_q8(const SChunk<kQ6K, NA>& ch, float* a
 
 // Input staging for the streaming kernels: 16-byte loads, four in flight per thread;
 // FP32 input goes to chunk_slot order, per-unit sums in natural order.
-template <int UNIT, bool Q8>
-__device__ void sstage(const MvArgs& a, float* xs, float* usum, float* red) {
+//
+// Inputs of up to 4 floats per thread with a norm take one pass: x, delta and the norm
+// weights are loaded together and the normalised input is written to LDS once.
+template <bool Q8>
+__device__ void sstage_normed(const MvArgs& a, float4* xs4, float* red) {
     const int n4 = a.cols / 4;
     const bool writer = a.x_out && blockIdx.x == 0;
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
     const float4* d4 = reinterpret_cast<const float4*>(a.delta);
-    float4* xs4 = reinterpret_cast<float4*>(xs);
+    const float4* n4p = reinterpret_cast<const float4*>(a.norm);
+    float4 v[4], w[4], dv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        if (i < n4) {
+            v[k] = x4[i];
+            if (d4) dv[k] = d4[i];
+            w[k] = n4p[i];
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        if (i < n4) {
+            if (d4) {
+                v[k].x += dv[k].x;
+                v[k].y += dv[k].y;
+                v[k].z += dv[k].z;
+                v[k].w += dv[k].w;
+            }
+            if (writer) reinterpret_cast<float4*>(a.x_out)[i] = v[k];
+            ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+        }
+    }
+    const float total = block_sum(ss, red);
+    const float scale = 1.f / sqrtf(total / (float)a.cols + a.eps);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        if (i < n4) {
+            float4 o;
+            o.x = v[k].x * (scale * w[k].x);
+            o.y = v[k].y * (scale * w[k].y);
+            o.z = v[k].z * (scale * w[k].z);
+            o.w = v[k].w * (scale * w[k].w);
+            xs4[Q8 ? i : chunk_slot(i)] = o;
+        }
+    }
+}
+
+template <bool Q8>
+__device__ void sstage_general(const MvArgs& a, float4* xs4, float* red) {
+    const int n4 = a.cols / 4;
+    const bool writer = a.x_out && blockIdx.x == 0;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    const float4* d4 = reinterpret_cast<const float4*>(a.delta);
     float ss = 0.f;
     for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * blockDim.x) {
         float4 v[4];
@@ -457,30 +507,36 @@ __device__ void sstage(const MvArgs& a, float* xs, float* usum, float* red) {
             }
         }
     }
-    if (a.norm) {
-        const float total = block_sum(ss, red);
-        const float scale = 1.f / sqrtf(total / (float)a.cols + a.eps);
-        const float4* n4p = reinterpret_cast<const float4*>(a.norm);
-        for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * blockDim.x) {
-            float4 w[4];
+    if (!a.norm) return;
+    const float total = block_sum(ss, red);
+    const float scale = 1.f / sqrtf(total / (float)a.cols + a.eps);
+    const float4* n4p = reinterpret_cast<const float4*>(a.norm);
+    for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * blockDim.x) {
+        float4 w[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (i0 + k * (int)blockDim.x < n4) w[k] = n4p[i0 + k * blockDim.x];
+        for (int k = 0; k < 4; ++k)
+            if (i0 + k * (int)blockDim.x < n4) w[k] = n4p[i0 + k * blockDim.x];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int i = i0 + k * blockDim.x;
-                if (i < n4) {
-                    const int sl = Q8 ? i : chunk_slot(i);
-                    float4 v = xs4[sl];
-                    v.x = v.x * (scale * w[k].x);
-                    v.y = v.y * (scale * w[k].y);
-                    v.z = v.z * (scale * w[k].z);
-                    v.w = v.w * (scale * w[k].w);
-                    xs4[sl] = v;
-                }
+        for (int k = 0; k < 4; ++k) {
+            const int i = i0 + k * blockDim.x;
+            if (i < n4) {
+                const int sl = Q8 ? i : chunk_slot(i);
+                float4 v = xs4[sl];
+                v.x = v.x * (scale * w[k].x);
+                v.y = v.y * (scale * w[k].y);
+                v.z = v.z * (scale * w[k].z);
+                v.w = v.w * (scale * w[k].w);
+                xs4[sl] = v;
             }
         }
     }
+}
+
+template <int UNIT, bool Q8>
+__device__ void sstage(const MvArgs& a, float* xs, float* usum, float* red) {
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+    if (a.norm && a.cols <= 16 * (int)blockDim.x) sstage_normed<Q8>(a, xs4, red);
+    else sstage_general<Q8>(a, xs4, red);
     __syncthreads();
     if constexpr (!Q8) {
         constexpr int U4 = UNIT / 4;
@@ -563,13 +619,29 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
         }
     };
 
+    // Conv epilogue operands of an item's rows, fetched with its weights: lane
+    // r*conv_width + j holds history slot j and tap j of row row0 + r.
+    auto conv_fetch = [&](int s, int r0, float& hv, float& kv) {
+        hv = 0.f;
+        kv = 0.f;
+        if (a.conv_w && s == 0) {
+            const int cw = a.conv_width, r = lane / cw, j = lane - r * cw, row = r0 + r;
+            if (r < R && row < a.seg[0].rows) {
+                hv = a.conv_state[(size_t)row * cw + j];
+                kv = a.conv_w[(size_t)row * cw + j];
+            }
+        }
+    };
+
     int g = blockIdx.x * 4 + wave, c = 0;
     const uint8_t* rp[NA];
     int seg = 0, row0 = 0;
     SChunk<T, NA> cur, nxt;
+    float conv_h = 0.f, conv_k = 0.f;
     if (g < a.groups) {
         rows_of(g, rp, seg, row0);
         sload<T, NA>(cur, rp, 0, lane);
+        conv_fetch(seg, row0, conv_h, conv_k);
     }
     sstage<UW, Q8>(a, xs, usum, red);
     if constexpr (Q8) {
@@ -591,10 +663,14 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
         }
         const uint8_t* rpn[NA];
         int segn = seg, row0n = row0;
+        float conv_hn = conv_h, conv_kn = conv_k;
 #pragma unroll
         for (int r = 0; r < NA; ++r) rpn[r] = rp[r];
         if (gn < a.groups) {
-            if (gn != g) rows_of(gn, rpn, segn, row0n);
+            if (gn != g) {
+                rows_of(gn, rpn, segn, row0n);
+                conv_fetch(segn, row0n, conv_hn, conv_kn);
+            }
             sload<T, NA>(nxt, rpn, cn, lane);
         }
         if constexpr (Q8) scompute_q8<NA>(cur, acc, xq, xscale, qsum, c, lane);
@@ -602,7 +678,24 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
         if (c == cpr - 1) {
 #pragma unroll
             for (int r = 0; r < NA; ++r) acc[r] = wave_sum(acc[r]);
-            if (lane == 0) {
+            if (!PAIR && a.conv_w && seg == 0) {
+                // causal conv1d + SiLU of the rows (backend.cpp:22-29): the history
+                // shifts left by one slot, the new value enters the last slot, and the
+                // taps are summed in slot order
+                const int cw = a.conv_width, r = lane / cw, j = lane - r * cw, row = row0 + r;
+                float v = 0.f;
+#pragma unroll
+                for (int rr = 0; rr < R; ++rr) v = r == rr ? acc[rr] : v;
+                const float shifted = __shfl_down(conv_h, 1, 64);
+                const float hn = j == cw - 1 ? v : shifted;
+                const float p = hn * conv_k;
+                float sum = 0.f;
+                for (int jj = 0; jj < cw; ++jj) sum += __shfl(p, lane - j + jj, 64);
+                if (r < R && row < a.seg[0].rows) {
+                    a.conv_state[(size_t)row * cw + j] = hn;
+                    if (j == 0) a.seg[0].y[row] = siluf_(sum);
+                }
+            } else if (lane == 0) {
                 const MvSeg sg = a.seg[seg];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
@@ -610,8 +703,6 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
                     if (row < sg.rows) {
                         if constexpr (PAIR) {
                             sg.y[row] = siluf_(acc[r]) * acc[(R + r) % NA];
-                        } else if (a.conv_w && seg == 0) {
-                            sg.y[row] = conv_step(a.conv_w, a.conv_state, a.conv_width, row, acc[r]);
                         } else {
                             sg.y[row] = acc[r];
                             if (a.mode == kMvArgmax) {
@@ -630,6 +721,8 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
         c = cn;
         seg = segn;
         row0 = row0n;
+        conv_h = conv_hn;
+        conv_k = conv_kn;
 #pragma unroll
         for (int r = 0; r < NA; ++r) rp[r] = rpn[r];
     }
@@ -701,6 +794,8 @@ template <int T, bool Q8, bool PAIR> static hipError_t launch_stream_r(const MvA
 hipError_t launch_matvec_stream(uint32_t type, bool q8, const MvArgs& a, hipStream_t stream) {
     const size_t lds = matvec_lds_bytes(type, a.cols, q8);
     const bool pair = a.mode == kMvSwiglu;
+    // the conv epilogue holds an item's rows x taps in the lanes of one wave
+    if (a.conv_w && (pair || a.conv_width < 1 || a.conv_width * a.rows_per_group > 64)) return hipErrorInvalidValue;
     if (type == kQ6K) {
         if (q8) return pair ? launch_stream_r<kQ6K, true, true>(a, lds, stream) : launch_stream_r<kQ6K, true, false>(a, lds, stream);
         return pair ? launch_stream_r<kQ6K, false, true>(a, lds, stream) : launch_stream_r<kQ6K, false, false>(a, lds, stream);
