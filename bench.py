@@ -93,6 +93,38 @@ def cpu_baseline(path: Path, seconds: float, context: int):
                       f"CPU path, OpenMP {threads} threads"}
 
 
+def copy_probe(mib: int):
+    """One device-to-device copy of `mib` MiB through the HIP runtime's copy kernel: the
+    known-size reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = mib << 20
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    for p in (src, dst):
+        if hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(n)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    if hip.hipMemset(src, 1, ctypes.c_size_t(n)) != 0 or hip.hipDeviceSynchronize() != 0:
+        raise RuntimeError("hipMemset failed")
+    for _ in range(3):
+        if hip.hipMemcpy(dst, src, ctypes.c_size_t(n), 3) != 0:  # hipMemcpyDeviceToDevice
+            raise RuntimeError("hipMemcpy failed")
+    hip.hipDeviceSynchronize()
+    hip.hipFree(src)
+    hip.hipFree(dst)
+    log(f"copied {mib} MiB device to device 3 times")
+
+
+def traffic_from_profiles(model: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `model` measured by the rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes committed under profiles/ (scaled by the copy-kernel calibration),
+    or None when no such measurement is committed."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text()).get(model, {}).get(kernel)
+    return None if rec is None else rec.get("bytes_per_launch")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,11 +139,16 @@ def main():
     ap.add_argument("--trace-steps", type=int, default=3)
     ap.add_argument("--no-graph", action="store_true",
                     help="launch every kernel from the host instead of replaying the step graph (for profilers)")
+    ap.add_argument("--copy-probe", type=int, metavar="MIB",
+                    help="only run a device-to-device copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU decode is not part of "
               "this build", file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
 
     import emprise_amd as ea
     path = model_file(args.model, seed=0)
@@ -181,7 +218,7 @@ def main():
                    "parallelism": "single GPU"},
         "hbm_roofline_fraction": round(e2e_gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(args.model, name), "kernel": name,
                      "bytes_per_launch": int(bpl), "us_per_launch": round(mspl * 1e3, 3),
                      "launches_per_step": launches // args.trace_steps},
         "cpu_baseline": cpu,

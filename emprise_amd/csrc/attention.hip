@@ -217,14 +217,14 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
     const int chunks = (a.context + kAttnChunk - 1) / kAttnChunk;
     const dim3 grid(a.kv_heads * chunks), block(kAttnWaves * 64);
     switch (a.head_dim) {
-    case 64: hipLaunchKernelGGL(attention_kernel<1>, grid, block, 0, stream, a); break;
-    case 128: hipLaunchKernelGGL(attention_kernel<2>, grid, block, 0, stream, a); break;
-    case 256: hipLaunchKernelGGL(attention_kernel<4>, grid, block, 0, stream, a); break;
+    case 64: launch_kernel(attention_kernel<1>, grid, block, 0, stream, a); break;
+    case 128: launch_kernel(attention_kernel<2>, grid, block, 0, stream, a); break;
+    case 256: launch_kernel(attention_kernel<4>, grid, block, 0, stream, a); break;
     default: return hipErrorInvalidValue;
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3((a.heads * a.head_dim + 255) / 256), dim3(256), 0, stream, a);
+    launch_kernel(attention_combine_kernel, dim3((a.heads * a.head_dim + 255) / 256), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -16,6 +16,8 @@
 
 using namespace emprise;
 
+thread_local TraceBracket emprise::g_trace_bracket;
+
 namespace {
 
 thread_local std::string g_error;
@@ -132,15 +134,18 @@ emprise_status launched(hipError_t e) {
     return EMPRISE_OK;
 }
 
-// Launches through `launch`; while tracing, brackets it with two events and records the
-// launch's algorithmic bytes.
+// Launches through `launch`; while tracing, the launch's kernels carry a start/stop
+// event pair on their dispatch packets and the op's algorithmic bytes are recorded.
 template <class F> emprise_status traced(emprise_hip* h, const char* kernel, uint64_t bytes, F launch) {
     if (!h->tracing) return launched(launch());
     hipEvent_t a = h->trace_event(), b = h->trace_event();
     if (!a || !b) return fail(EMPRISE_EDEVICE, "trace event");
-    HIP_TRY(hipEventRecord(a, h->stream));
-    TRY(launched(launch()));
-    HIP_TRY(hipEventRecord(b, h->stream));
+    g_trace_bracket = {a, b};
+    const hipError_t e = launch();
+    const bool started = g_trace_bracket.start == nullptr;  // at least one kernel took the bracket
+    g_trace_bracket = {};
+    TRY(launched(e));
+    if (!started) return fail(EMPRISE_EDEVICE, "traced op '%s' launched no kernel", kernel);
     h->trace.push_back({kernel, bytes, a, b});
     return EMPRISE_OK;
 }

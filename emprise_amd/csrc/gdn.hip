@@ -117,15 +117,15 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_kernel(GdnArgs a) {
 
 hipError_t launch_delta_conv(const float* qkv, const float* conv_w, float* conv_state, float* out, int channels,
                              int conv_width, hipStream_t stream) {
-    hipLaunchKernelGGL(delta_conv_kernel, dim3((channels + 255) / 256), dim3(256), 0, stream, qkv, conv_w, conv_state,
+    launch_kernel(delta_conv_kernel, dim3((channels + 255) / 256), dim3(256), 0, stream, qkv, conv_w, conv_state,
                        out, channels, conv_width);
     return hipGetLastError();
 }
 
 hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream) {
     const dim3 grid(a.value_heads), block(kGdnWaves * 64);
-    if (a.state_dim == 64) hipLaunchKernelGGL(gdn_kernel<1>, grid, block, 0, stream, a);
-    else if (a.state_dim == 128) hipLaunchKernelGGL(gdn_kernel<2>, grid, block, 0, stream, a);
+    if (a.state_dim == 64) launch_kernel(gdn_kernel<1>, grid, block, 0, stream, a);
+    else if (a.state_dim == 128) launch_kernel(gdn_kernel<2>, grid, block, 0, stream, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

@@ -1,10 +1,31 @@
 // Host-side launch interface of the gfx950 kernels (internal to libemprise_hip.so).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stddef.h>
 #include <stdint.h>
 
 namespace emprise {
+
+// Kernel timing bracket of the launch trace. While `stop` is set, launch_kernel puts the
+// events on the dispatch packets themselves (hipExtLaunchKernelGGL): the first launch
+// records `start` as it begins and every launch records `stop` as it ends, so a traced
+// span is the kernels' own execution time, with no extra packets in the queue.
+struct TraceBracket {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local TraceBracket g_trace_bracket;
+
+template <typename F, typename... Args>
+inline void launch_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
+    TraceBracket& t = g_trace_bracket;
+    if (t.stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, t.start, t.stop, 0, args...);
+        t.start = nullptr;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+    }
+}
 
 constexpr int kMaxSeg = 8;
 constexpr int kMvRows = 2;            // rows per wave iteration (unit-major rows)

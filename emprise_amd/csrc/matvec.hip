@@ -757,7 +757,7 @@ template <class K> hipError_t launch_stream(K kernel, const MvArgs& a, size_t ld
     const int cap = resident_blocks(kernel, lds);
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), lds, stream, a);
+    launch_kernel(kernel, dim3(blocks), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 
@@ -894,20 +894,20 @@ hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, 
     switch (type) {
     case kQ6K:
         if (q8) {
-            if (pair) hipLaunchKernelGGL((matvec_kernel<kQ6K, kMvRows, true, true>), grid, block, lds, stream, a);
-            else hipLaunchKernelGGL((matvec_kernel<kQ6K, kMvRows, true, false>), grid, block, lds, stream, a);
+            if (pair) launch_kernel((matvec_kernel<kQ6K, kMvRows, true, true>), grid, block, lds, stream, a);
+            else launch_kernel((matvec_kernel<kQ6K, kMvRows, true, false>), grid, block, lds, stream, a);
         } else {
-            if (pair) hipLaunchKernelGGL((matvec_kernel<kQ6K, kMvRows, false, true>), grid, block, lds, stream, a);
-            else hipLaunchKernelGGL((matvec_kernel<kQ6K, kMvRows, false, false>), grid, block, lds, stream, a);
+            if (pair) launch_kernel((matvec_kernel<kQ6K, kMvRows, false, true>), grid, block, lds, stream, a);
+            else launch_kernel((matvec_kernel<kQ6K, kMvRows, false, false>), grid, block, lds, stream, a);
         }
         break;
     case kQ4K:
-        if (pair) hipLaunchKernelGGL((matvec_kernel<kQ4K, kMvRows, false, true>), grid, block, lds, stream, a);
-        else hipLaunchKernelGGL((matvec_kernel<kQ4K, kMvRows, false, false>), grid, block, lds, stream, a);
+        if (pair) launch_kernel((matvec_kernel<kQ4K, kMvRows, false, true>), grid, block, lds, stream, a);
+        else launch_kernel((matvec_kernel<kQ4K, kMvRows, false, false>), grid, block, lds, stream, a);
         break;
-    case kF32: hipLaunchKernelGGL((matvec_raw_kernel<kF32>), grid, block, lds, stream, a); break;
-    case kF16: hipLaunchKernelGGL((matvec_raw_kernel<kF16>), grid, block, lds, stream, a); break;
-    case kBF16: hipLaunchKernelGGL((matvec_raw_kernel<kBF16>), grid, block, lds, stream, a); break;
+    case kF32: launch_kernel((matvec_raw_kernel<kF32>), grid, block, lds, stream, a); break;
+    case kF16: launch_kernel((matvec_raw_kernel<kF16>), grid, block, lds, stream, a); break;
+    case kBF16: launch_kernel((matvec_raw_kernel<kBF16>), grid, block, lds, stream, a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -919,7 +919,7 @@ hipError_t launch_dequant_rows(const uint8_t* w, uint32_t type, int cols, uint64
     uint64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, w, type, cols, row0, n, out);
+    launch_kernel(dequant_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, w, type, cols, row0, n, out);
     return hipGetLastError();
 }
 

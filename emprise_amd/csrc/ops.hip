@@ -106,46 +106,46 @@ unsigned grid_for(size_t n, unsigned block, unsigned cap) {
 }  // namespace
 
 hipError_t launch_fill(float* dst, float value, size_t n, hipStream_t stream) {
-    hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n, 256, 4096)), dim3(256), 0, stream, dst, value, n);
+    launch_kernel(fill_kernel, dim3(grid_for(n, 256, 4096)), dim3(256), 0, stream, dst, value, n);
     return hipGetLastError();
 }
 hipError_t launch_fill_u64(unsigned long long* dst, unsigned long long value, size_t n, hipStream_t stream) {
-    hipLaunchKernelGGL(fill_u64_kernel, dim3(grid_for(n, 256, 4096)), dim3(256), 0, stream, dst, value, n);
+    launch_kernel(fill_u64_kernel, dim3(grid_for(n, 256, 4096)), dim3(256), 0, stream, dst, value, n);
     return hipGetLastError();
 }
 hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t stream) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, stream, x, w, out, n, eps);
+    launch_kernel(rmsnorm_kernel, dim3(1), dim3(1024), 0, stream, x, w, out, n, eps);
     return hipGetLastError();
 }
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream) {
-    hipLaunchKernelGGL(add_kernel, dim3(grid_for((size_t)n, 256, 1u << 20)), dim3(256), 0, stream, x, y, n);
+    launch_kernel(add_kernel, dim3(grid_for((size_t)n, 256, 1u << 20)), dim3(256), 0, stream, x, y, n);
     return hipGetLastError();
 }
 hipError_t launch_swiglu(float* gate, const float* up, int n, hipStream_t stream) {
-    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for((size_t)n, 256, 1u << 20)), dim3(256), 0, stream, gate, up, n);
+    launch_kernel(swiglu_kernel, dim3(grid_for((size_t)n, 256, 1u << 20)), dim3(256), 0, stream, gate, up, n);
     return hipGetLastError();
 }
 hipError_t launch_embed(const uint8_t* w, uint32_t type, int cols, int rows, const int* token, float* out,
                         hipStream_t stream) {
-    hipLaunchKernelGGL(embed_kernel, dim3(grid_for((size_t)cols, 256, 64)), dim3(256), 0, stream, w, type, cols, rows,
+    launch_kernel(embed_kernel, dim3(grid_for((size_t)cols, 256, 64)), dim3(256), 0, stream, w, type, cols, rows,
                        token, out);
     return hipGetLastError();
 }
 hipError_t launch_argmax(const float* logits, int n, unsigned long long*, int* index, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, stream, logits, n, index);
+    launch_kernel(argmax_kernel, dim3(1), dim3(1024), 0, stream, logits, n, index);
     return hipGetLastError();
 }
 hipError_t launch_argmax_finish(const unsigned long long* key, int* index, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(64), 0, stream, const_cast<unsigned long long*>(key), index);
+    launch_kernel(argmax_finish_kernel, dim3(1), dim3(64), 0, stream, const_cast<unsigned long long*>(key), index);
     return hipGetLastError();
 }
 hipError_t launch_quantize_q8(const float* x, int cols, int8_t* q, float* scales, hipStream_t stream) {
-    hipLaunchKernelGGL(quantize_q8_kernel, dim3(grid_for((size_t)cols / 32, 64, 1u << 20)), dim3(64), 0, stream, x,
+    launch_kernel(quantize_q8_kernel, dim3(grid_for((size_t)cols / 32, 64, 1u << 20)), dim3(64), 0, stream, x,
                        cols, q, scales);
     return hipGetLastError();
 }
 hipError_t launch_advance(int* state, const int* prompt, int* history, const int* next, hipStream_t stream) {
-    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, state, prompt, history, next);
+    launch_kernel(advance_kernel, dim3(1), dim3(64), 0, stream, state, prompt, history, next);
     return hipGetLastError();
 }
 
