@@ -307,18 +307,22 @@ template <int NA> struct SChunk<kQ4K, NA> {
 };
 
 // Weight bytes are read once per token: non-temporal loads stream them past the caches.
+// The pointers are cast to the global address space so the loads are global_load_*:
+// through a generic pointer they become flat_load_*, which also count against lgkmcnt,
+// so every wait for an LDS read would drain the next item's weight loads as well.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+#define EMPRISE_GLOBAL __attribute__((address_space(1)))
 __device__ __forceinline__ uint4 nt_u4(const uint8_t* p) {
-    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    const u32x4_t v = __builtin_nontemporal_load((const EMPRISE_GLOBAL u32x4_t*)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint32_t nt_u32(const uint8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    return __builtin_nontemporal_load((const EMPRISE_GLOBAL uint32_t*)p);
 }
 __device__ __forceinline__ uint32_t nt_u16(const uint8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+    return __builtin_nontemporal_load((const EMPRISE_GLOBAL uint16_t*)p);
 }
-__device__ __forceinline__ uint32_t nt_u8(const uint8_t* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ uint32_t nt_u8(const uint8_t* p) { return __builtin_nontemporal_load((const EMPRISE_GLOBAL uint8_t*)p); }
 
 template <int T, int NA>
 __device__ __forceinline__ void sload(SChunk<T, NA>& ch, const uint8_t* const* rp, int c, int lane) {
@@ -474,38 +478,54 @@ __device__ void sstage_normed(const MvArgs& a, float4* xs4, float* red) {
     }
 }
 
-template <bool Q8>
-__device__ void sstage_general(const MvArgs& a, float4* xs4, float* red) {
+// B float4 per thread per batch. Every load of a batch is issued before any is used
+// (indices are clamped to the last float4, so no load sits under a branch): one memory
+// round trip per batch.
+template <bool Q8, int B>
+__device__ float sstage_batch(const MvArgs& a, float4* xs4, int i0) {
     const int n4 = a.cols / 4;
     const bool writer = a.x_out && blockIdx.x == 0;
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
     const float4* d4 = reinterpret_cast<const float4*>(a.delta);
+    float4 v[B];
+#pragma unroll
+    for (int k = 0; k < B; ++k) v[k] = x4[min(i0 + k * (int)blockDim.x, n4 - 1)];
+    if (d4) {
+        float4 dv[B];
+#pragma unroll
+        for (int k = 0; k < B; ++k) dv[k] = d4[min(i0 + k * (int)blockDim.x, n4 - 1)];
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            v[k].x += dv[k].x;
+            v[k].y += dv[k].y;
+            v[k].z += dv[k].z;
+            v[k].w += dv[k].w;
+        }
+    }
     float ss = 0.f;
-    for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * blockDim.x) {
-        float4 v[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = i0 + k * blockDim.x;
-            if (i < n4) {
-                v[k] = x4[i];
-                if (d4) {
-                    const float4 dv = d4[i];
-                    v[k].x += dv.x;
-                    v[k].y += dv.y;
-                    v[k].z += dv.z;
-                    v[k].w += dv.w;
-                }
-            }
+    for (int k = 0; k < B; ++k) {
+        const int i = i0 + k * blockDim.x;
+        if (i < n4) {
+            if (writer) reinterpret_cast<float4*>(a.x_out)[i] = v[k];
+            xs4[Q8 ? i : chunk_slot(i)] = v[k];
+            ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
         }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = i0 + k * blockDim.x;
-            if (i < n4) {
-                if (writer) reinterpret_cast<float4*>(a.x_out)[i] = v[k];
-                xs4[Q8 ? i : chunk_slot(i)] = v[k];
-                ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
-            }
-        }
+    }
+    return ss;
+}
+
+template <bool Q8>
+__device__ void sstage_general(const MvArgs& a, float4* xs4, float* red) {
+    const int n4 = a.cols / 4;
+    float ss = 0.f;
+    if (!a.delta && n4 <= 6 * (int)blockDim.x) {
+        ss = sstage_batch<Q8, 6>(a, xs4, threadIdx.x);  // up to 6144 columns in one round trip
+    } else if (!a.delta && n4 <= 12 * (int)blockDim.x) {
+        ss = sstage_batch<Q8, 6>(a, xs4, threadIdx.x);  // up to 12288 columns in two
+        ss += sstage_batch<Q8, 6>(a, xs4, threadIdx.x + 6 * blockDim.x);
+    } else {
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * blockDim.x) ss += sstage_batch<Q8, 4>(a, xs4, i0);
     }
     if (!a.norm) return;
     const float total = block_sum(ss, red);
@@ -514,8 +534,7 @@ __device__ void sstage_general(const MvArgs& a, float4* xs4, float* red) {
     for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * blockDim.x) {
         float4 w[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (i0 + k * (int)blockDim.x < n4) w[k] = n4p[i0 + k * blockDim.x];
+        for (int k = 0; k < 4; ++k) w[k] = n4p[min(i0 + k * (int)blockDim.x, n4 - 1)];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int i = i0 + k * blockDim.x;
@@ -586,13 +605,111 @@ __device__ void sstage_q8(int n, const float* xs, int8_t* xq, float* xscale, int
     }
 }
 
-template <int T, int R, bool Q8, bool PAIR>
-__global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
+// Work item of the streaming kernel: row group g (R rows, or R gate/up row pairs) x
+// 4096-column chunk c, with the row pointers of the group and, for the conv epilogue,
+// lane r*conv_width + j's history slot j and tap j of row row0 + r.
+template <int NA> struct SItem {
+    int g, c, seg, row0;
+    const uint8_t* rp[NA];
+    float conv_h, conv_k;
+};
+
+// Input registers of the one-shot staging: SB float4 per thread of x, and with DN of
+// the residual delta and the norm weights.
+template <int SB, bool DN> struct SInput {
+    float4 x[SB];
+    float4 d[DN ? SB : 1], w[DN ? SB : 1];
+};
+
+template <int SB, bool DN>
+__device__ __forceinline__ void sinput_issue(const MvArgs& a, SInput<SB, DN>& s) {
+    const int n4 = a.cols / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+#pragma unroll
+    for (int k = 0; k < SB; ++k) s.x[k] = x4[min((int)threadIdx.x + k * (int)blockDim.x, n4 - 1)];
+    if constexpr (DN) {
+        if (a.delta) {
+            const float4* d4 = reinterpret_cast<const float4*>(a.delta);
+#pragma unroll
+            for (int k = 0; k < SB; ++k) s.d[k] = d4[min((int)threadIdx.x + k * (int)blockDim.x, n4 - 1)];
+        }
+        if (a.norm) {
+            const float4* w4 = reinterpret_cast<const float4*>(a.norm);
+#pragma unroll
+            for (int k = 0; k < SB; ++k) s.w[k] = w4[min((int)threadIdx.x + k * (int)blockDim.x, n4 - 1)];
+        }
+    }
+}
+
+// Finishes the one-shot staging from registers: residual add (workgroup 0 writes
+// x_out), RMSNorm, the LDS store (chunk_slot order; natural order for Q8) and the
+// per-unit input sums, reduced across the UNIT/4 consecutive threads that hold a unit.
+template <int UNIT, bool Q8, int SB, bool DN>
+__device__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, float* usum, float* red) {
+    const int n4 = a.cols / 4;
+    const bool writer = a.x_out && blockIdx.x == 0;
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+    if constexpr (DN) {
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+            const int i = threadIdx.x + k * blockDim.x;
+            if (a.delta) {
+                s.x[k].x += s.d[k].x;
+                s.x[k].y += s.d[k].y;
+                s.x[k].z += s.d[k].z;
+                s.x[k].w += s.d[k].w;
+            }
+            if (i < n4) {
+                if (writer) reinterpret_cast<float4*>(a.x_out)[i] = s.x[k];
+                ss += s.x[k].x * s.x[k].x + s.x[k].y * s.x[k].y + s.x[k].z * s.x[k].z + s.x[k].w * s.x[k].w;
+            }
+        }
+        if (a.norm) {
+            const float total = block_sum(ss, red);
+            const float scale = 1.f / sqrtf(total / (float)a.cols + a.eps);
+#pragma unroll
+            for (int k = 0; k < SB; ++k) {
+                s.x[k].x = s.x[k].x * (scale * s.w[k].x);
+                s.x[k].y = s.x[k].y * (scale * s.w[k].y);
+                s.x[k].z = s.x[k].z * (scale * s.w[k].z);
+                s.x[k].w = s.x[k].w * (scale * s.w[k].w);
+            }
+        }
+    }
+    constexpr int U4 = UNIT / 4;
+#pragma unroll
+    for (int k = 0; k < SB; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        if (i < n4) xs4[Q8 ? i : chunk_slot(i)] = s.x[k];
+        if constexpr (!Q8) {
+            float t = (s.x[k].x + s.x[k].y) + (s.x[k].z + s.x[k].w);
+            t += __shfl_xor(t, 1, 64);
+            t += __shfl_xor(t, 2, 64);
+            if constexpr (U4 == 8) t += __shfl_xor(t, 4, 64);
+            if (i < n4 && (i & (U4 - 1)) == 0) usum[i / U4] = t;
+        }
+    }
+}
+
+// Staging modes of a launch: 0 generic (sstage, after the first items' loads),
+// 1 up to 4096 columns with residual add and norm, 2 up to 12288 columns, plain input.
+constexpr int kStreamWaves = 8;
+template <int SM> struct StageMode;
+template <> struct StageMode<0> { static constexpr int sb = 1; static constexpr bool dn = false; };
+template <> struct StageMode<1> { static constexpr int sb = 1024 / (kStreamWaves * 64); static constexpr bool dn = true; };
+template <> struct StageMode<2> { static constexpr int sb = 3072 / (kStreamWaves * 64); static constexpr bool dn = false; };
+
+template <int T, bool Q8, bool PAIR, bool CONV, int SM>
+__global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ float red[16];
+    __shared__ float red[kStreamWaves];
     __shared__ unsigned long long block_best;
+    constexpr int R = PAIR ? kMvStreamPairRows : kMvStreamRows;
     constexpr int UW = Fmt<T>::unit;
     constexpr int NA = PAIR ? R * 2 : R;
+    constexpr int SB = StageMode<SM>::sb;
+    constexpr bool DN = StageMode<SM>::dn;
     float* xs = reinterpret_cast<float*>(smem);
     float* usum = xs + a.cols;
     const int units = a.cols / UW;
@@ -604,46 +721,74 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int cpr = a.cols / kChunkCols;
     const size_t row_bytes = (size_t)(a.cols / 256) * Fmt<T>::block;
-    const int stride = gridDim.x * 4;
+    const int stride = gridDim.x * kStreamWaves;
+    const uint8_t* dummy = reinterpret_cast<const uint8_t*>(a.x);
 
-    auto rows_of = [&](int g, const uint8_t** rp, int& s, int& row0) {
-        s = 0;
-        while (s + 1 < a.nseg && g >= a.seg[s + 1].g0) ++s;
-        row0 = (g - a.seg[s].g0) * R;
+    // row pointers of item `it`'s row group
+    auto rows_of = [&](SItem<NA>& it) {
+        int s = 0;
+        while (s + 1 < a.nseg && it.g >= a.seg[s + 1].g0) ++s;
+        it.seg = s;
+        it.row0 = (it.g - a.seg[s].g0) * R;
         const int nrows = a.seg[s].rows;
 #pragma unroll
         for (int r = 0; r < NA; ++r) {
-            const int rr = r < R ? row0 + r : row0 + r - R;
+            const int rr = r < R ? it.row0 + r : it.row0 + r - R;
             const int rc = rr < nrows ? rr : nrows - 1;
-            rp[r] = (r < R ? a.seg[s].w : a.seg[1].w) + (size_t)rc * row_bytes;
+            it.rp[r] = (r < R ? a.seg[s].w : a.seg[1].w) + (size_t)rc * row_bytes;
+        }
+    };
+    // moves `it` n items ahead in this wave's sequence (n <= 2 * chunks per row)
+    auto skip = [&](SItem<NA>& it, int n) {
+        const int c = it.c + n, hop = c / cpr;
+        it.c = c - hop * cpr;
+        if (hop) {
+            it.g += hop * stride;
+            if (it.g < a.groups) rows_of(it);
+        }
+    };
+    // Issues the loads of item `it` into `buf`. The same instructions run for every
+    // item -- one past the end reads the input vector instead (L2-resident, never
+    // used) -- so the compiler's wait counts stay exact and a wave never waits for
+    // more than the buffer it is about to compute.
+    auto iload = [&](SChunk<T, NA>& buf, SItem<NA>& it) {
+        const bool valid = it.g < a.groups;
+        const uint8_t* p[NA];
+#pragma unroll
+        for (int r = 0; r < NA; ++r) p[r] = valid ? it.rp[r] : dummy;
+        sload<T, NA>(buf, p, valid ? it.c : 0, lane);
+        if constexpr (CONV) {
+            const int cw = a.conv_width, r = lane / cw, j = lane - r * cw, row = it.row0 + r;
+            const bool on = valid && it.seg == 0 && r < R && row < a.seg[0].rows;
+            const size_t o = on ? (size_t)row * cw + j : 0;
+            const float h = *(on ? a.conv_state + o : a.x), k = *(on ? a.conv_w + o : a.x);
+            it.conv_h = on ? h : 0.f;
+            it.conv_k = on ? k : 0.f;
         }
     };
 
-    // Conv epilogue operands of an item's rows, fetched with its weights: lane
-    // r*conv_width + j holds history slot j and tap j of row row0 + r.
-    auto conv_fetch = [&](int s, int r0, float& hv, float& kv) {
-        hv = 0.f;
-        kv = 0.f;
-        if (a.conv_w && s == 0) {
-            const int cw = a.conv_width, r = lane / cw, j = lane - r * cw, row = r0 + r;
-            if (r < R && row < a.seg[0].rows) {
-                hv = a.conv_state[(size_t)row * cw + j];
-                kv = a.conv_w[(size_t)row * cw + j];
-            }
-        }
-    };
+    // Input loads first, then the weights of the wave's first two items, then the
+    // staging arithmetic: the loads return in issue order, so the staging waits only
+    // for its own (L2-resident) data while the weight streams are in flight.
+    // (sched_barrier keeps the three groups of loads in this order: the wait for
+    // buffer A must not cover any of B's loads.)
+    SInput<SB, DN> sin;
+    if constexpr (SM != 0) sinput_issue<SB, DN>(a, sin);
+    SItem<NA> ia, ib;
+    ia.g = blockIdx.x * kStreamWaves + wave;
+    ia.c = 0;
+    if (ia.g < a.groups) rows_of(ia);
+    ib = ia;
+    skip(ib, 1);
+    SChunk<T, NA> A, B;
+    __builtin_amdgcn_sched_barrier(0);
+    iload(A, ia);
+    __builtin_amdgcn_sched_barrier(0);
+    iload(B, ib);
+    __builtin_amdgcn_sched_barrier(0);
 
-    int g = blockIdx.x * 4 + wave, c = 0;
-    const uint8_t* rp[NA];
-    int seg = 0, row0 = 0;
-    SChunk<T, NA> cur, nxt;
-    float conv_h = 0.f, conv_k = 0.f;
-    if (g < a.groups) {
-        rows_of(g, rp, seg, row0);
-        sload<T, NA>(cur, rp, 0, lane);
-        conv_fetch(seg, row0, conv_h, conv_k);
-    }
-    sstage<UW, Q8>(a, xs, usum, red);
+    if constexpr (SM != 0) sinput_finish<UW, Q8, SB, DN>(a, sin, xs, usum, red);
+    else sstage<UW, Q8>(a, xs, usum, red);
     if constexpr (Q8) {
         __syncthreads();
         sstage_q8(a.cols, xs, xq, xscale, qsum);
@@ -655,40 +800,26 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
     float acc[NA];
 #pragma unroll
     for (int r = 0; r < NA; ++r) acc[r] = 0.f;
-    while (g < a.groups) {
-        int gn = g, cn = c + 1;
-        if (cn == cpr) {
-            cn = 0;
-            gn = g + stride;
-        }
-        const uint8_t* rpn[NA];
-        int segn = seg, row0n = row0;
-        float conv_hn = conv_h, conv_kn = conv_k;
-#pragma unroll
-        for (int r = 0; r < NA; ++r) rpn[r] = rp[r];
-        if (gn < a.groups) {
-            if (gn != g) {
-                rows_of(gn, rpn, segn, row0n);
-                conv_fetch(segn, row0n, conv_hn, conv_kn);
-            }
-            sload<T, NA>(nxt, rpn, cn, lane);
-        }
-        if constexpr (Q8) scompute_q8<NA>(cur, acc, xq, xscale, qsum, c, lane);
-        else scompute<T, NA>(cur, acc, xs, usum, c, lane);
-        if (c == cpr - 1) {
+
+    // Computes the item held in `buf`, runs the row epilogue after a row group's last
+    // chunk, then refills `buf` with the item two ahead (the other buffer holds the next).
+    auto process = [&](SChunk<T, NA>& buf, SItem<NA>& it) {
+        if constexpr (Q8) scompute_q8<NA>(buf, acc, xq, xscale, qsum, it.c, lane);
+        else scompute<T, NA>(buf, acc, xs, usum, it.c, lane);
+        if (it.c == cpr - 1) {
 #pragma unroll
             for (int r = 0; r < NA; ++r) acc[r] = wave_sum(acc[r]);
-            if (!PAIR && a.conv_w && seg == 0) {
+            if (CONV && it.seg == 0) {
                 // causal conv1d + SiLU of the rows (backend.cpp:22-29): the history
                 // shifts left by one slot, the new value enters the last slot, and the
                 // taps are summed in slot order
-                const int cw = a.conv_width, r = lane / cw, j = lane - r * cw, row = row0 + r;
+                const int cw = a.conv_width, r = lane / cw, j = lane - r * cw, row = it.row0 + r;
                 float v = 0.f;
 #pragma unroll
                 for (int rr = 0; rr < R; ++rr) v = r == rr ? acc[rr] : v;
-                const float shifted = __shfl_down(conv_h, 1, 64);
+                const float shifted = __shfl_down(it.conv_h, 1, 64);
                 const float hn = j == cw - 1 ? v : shifted;
-                const float p = hn * conv_k;
+                const float p = hn * it.conv_k;
                 float sum = 0.f;
                 for (int jj = 0; jj < cw; ++jj) sum += __shfl(p, lane - j + jj, 64);
                 if (r < R && row < a.seg[0].rows) {
@@ -696,10 +827,10 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
                     if (j == 0) a.seg[0].y[row] = siluf_(sum);
                 }
             } else if (lane == 0) {
-                const MvSeg sg = a.seg[seg];
+                const MvSeg sg = a.seg[it.seg];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const int row = row0 + r;
+                    const int row = it.row0 + r;
                     if (row < sg.rows) {
                         if constexpr (PAIR) {
                             sg.y[row] = siluf_(acc[r]) * acc[(R + r) % NA];
@@ -716,15 +847,13 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
 #pragma unroll
             for (int r = 0; r < NA; ++r) acc[r] = 0.f;
         }
-        cur = nxt;
-        g = gn;
-        c = cn;
-        seg = segn;
-        row0 = row0n;
-        conv_h = conv_hn;
-        conv_k = conv_kn;
-#pragma unroll
-        for (int r = 0; r < NA; ++r) rp[r] = rpn[r];
+        skip(it, 2);
+        iload(buf, it);
+    };
+    while (ia.g < a.groups) {
+        process(A, ia);
+        if (ib.g >= a.groups) break;
+        process(B, ib);
     }
     if (a.mode == kMvArgmax) {
         if (lane == 0 && best) atomicMax(&block_best, best);
@@ -734,8 +863,7 @@ __global__ __launch_bounds__(256) void matvec_stream_kernel(MvArgs a) {
 }
 
 // Workgroups of a streaming launch: one full round of resident workgroups (occupancy x
-// CUs), so every wave keeps two items in flight and none waits for a second round.
-// EMPRISE_MV_WAVES_PER_CU (resident waves per CU to aim for) overrides it for sweeps.
+// CUs), so no wave waits for a second dispatch round.
 template <class K> int resident_blocks(K kernel, size_t lds) {
     static int cached = 0;
     if (!cached) {
@@ -743,64 +871,58 @@ template <class K> int resident_blocks(K kernel, size_t lds) {
         hipDeviceProp_t prop;
         (void)hipGetDevice(&dev);
         (void)hipGetDeviceProperties(&prop, dev);
-        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), 256, lds);
-        const char* e = getenv("EMPRISE_MV_WAVES_PER_CU");
-        const int want = e ? atoi(e) / 4 : 0;
-        if (want > 0 && want < per_cu) per_cu = want;
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
+                                                           kStreamWaves * 64, lds);
         cached = (per_cu > 0 ? per_cu : 1) * prop.multiProcessorCount;
     }
     return cached;
 }
 
 template <class K> hipError_t launch_stream(K kernel, const MvArgs& a, size_t lds, hipStream_t stream) {
-    int blocks = (a.groups + 3) / 4;
+    int blocks = (a.groups + kStreamWaves - 1) / kStreamWaves;
     const int cap = resident_blocks(kernel, lds);
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
-    launch_kernel(kernel, dim3(blocks), dim3(256), lds, stream, a);
+    launch_kernel(kernel, dim3(blocks), dim3(kStreamWaves * 64), lds, stream, a);
     return hipGetLastError();
+}
+
+template <int T, bool Q8, bool PAIR, bool CONV>
+hipError_t launch_stream_mode(const MvArgs& a, size_t lds, hipStream_t stream) {
+    const int threads = kStreamWaves * 64, n4 = a.cols / 4;
+    if (n4 <= StageMode<1>::sb * threads) return launch_stream(matvec_stream_kernel<T, Q8, PAIR, CONV, 1>, a, lds, stream);
+    if constexpr (!CONV) {
+        if (!a.delta && !a.norm && n4 <= StageMode<2>::sb * threads)
+            return launch_stream(matvec_stream_kernel<T, Q8, PAIR, false, 2>, a, lds, stream);
+    }
+    return launch_stream(matvec_stream_kernel<T, Q8, PAIR, CONV, 0>, a, lds, stream);
+}
+
+template <int T, bool Q8> hipError_t launch_stream_kind(const MvArgs& a, size_t lds, hipStream_t stream) {
+    if (a.mode == kMvSwiglu) return launch_stream_mode<T, Q8, true, false>(a, lds, stream);
+    if (a.conv_w) return launch_stream_mode<T, Q8, false, true>(a, lds, stream);
+    return launch_stream_mode<T, Q8, false, false>(a, lds, stream);
 }
 
 }  // namespace
 
-// Rows per item of the streaming kernel: 2 rows (2 gate/up pairs) -- measured against 1
-// and 4 on the 9B shapes; more rows amortise the input reads, fewer spread the work. EMPRISE_MV_ROWS (1, 2 or 4) overrides it
-// for launch-shape sweeps.
+// Rows per item of the streaming kernel: 2 rows (2 gate/up pairs), chosen by sweep
+// against 1 and 4 on the 9B shapes.
 int matvec_rows_per_group(uint32_t type, uint64_t cols, int mode, uint64_t total_rows) {
     (void)total_rows;
-    if ((type == kQ6K || type == kQ4K) && cols % kChunkCols == 0) {
-        static const int forced = [] {
-            const char* e = getenv("EMPRISE_MV_ROWS");
-            const int v = e ? atoi(e) : 0;
-            return (v == 1 || v == 2 || v == 4) ? v : 0;
-        }();
-        if (mode == kMvSwiglu) return forced ? (forced > 2 ? 2 : forced) : kMvStreamPairRows;
-        return forced ? forced : kMvStreamRows;
-    }
+    if ((type == kQ6K || type == kQ4K) && cols % kChunkCols == 0)
+        return mode == kMvSwiglu ? kMvStreamPairRows : kMvStreamRows;
     return (type == kQ6K || type == kQ4K) ? kMvRows : 1;
-}
-
-template <int T, bool Q8, bool PAIR> static hipError_t launch_stream_r(const MvArgs& a, size_t lds, hipStream_t stream) {
-    switch (a.rows_per_group) {
-    case 1: return launch_stream(matvec_stream_kernel<T, 1, Q8, PAIR>, a, lds, stream);
-    case 2: return launch_stream(matvec_stream_kernel<T, 2, Q8, PAIR>, a, lds, stream);
-    case 4:
-        if constexpr (!PAIR) return launch_stream(matvec_stream_kernel<T, 4, Q8, PAIR>, a, lds, stream);
-        return hipErrorInvalidValue;
-    default: return hipErrorInvalidValue;
-    }
 }
 
 hipError_t launch_matvec_stream(uint32_t type, bool q8, const MvArgs& a, hipStream_t stream) {
     const size_t lds = matvec_lds_bytes(type, a.cols, q8);
-    const bool pair = a.mode == kMvSwiglu;
+    if (a.rows_per_group != (a.mode == kMvSwiglu ? kMvStreamPairRows : kMvStreamRows)) return hipErrorInvalidValue;
     // the conv epilogue holds an item's rows x taps in the lanes of one wave
-    if (a.conv_w && (pair || a.conv_width < 1 || a.conv_width * a.rows_per_group > 64)) return hipErrorInvalidValue;
-    if (type == kQ6K) {
-        if (q8) return pair ? launch_stream_r<kQ6K, true, true>(a, lds, stream) : launch_stream_r<kQ6K, true, false>(a, lds, stream);
-        return pair ? launch_stream_r<kQ6K, false, true>(a, lds, stream) : launch_stream_r<kQ6K, false, false>(a, lds, stream);
-    }
-    return pair ? launch_stream_r<kQ4K, false, true>(a, lds, stream) : launch_stream_r<kQ4K, false, false>(a, lds, stream);
+    if (a.conv_w && (a.mode == kMvSwiglu || a.conv_width < 1 || a.conv_width * a.rows_per_group > 64))
+        return hipErrorInvalidValue;
+    if (type == kQ6K) return q8 ? launch_stream_kind<kQ6K, true>(a, lds, stream) : launch_stream_kind<kQ6K, false>(a, lds, stream);
+    return launch_stream_kind<kQ4K, false>(a, lds, stream);
 }
 
 namespace {
