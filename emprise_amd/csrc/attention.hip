@@ -20,7 +20,8 @@
 // (E = 4) access per lane.
 //
 // The grid covers the whole context so the launch can be replayed from a hipGraph:
-// the position is read from device memory and chunks past it return at once.
+// the position is read from device memory and chunks past it return at once. Barriers
+// order LDS only (lds_barrier), so none of them waits for the K/V rows in flight.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         }
     }
     if (threadIdx.x < HD) vnew[threadIdx.x] = vin_d;
-    __syncthreads();
+    lds_barrier();
     // NEOX RoPE over the first `rotary` dims (model.cpp:121-127); one thread per pair.
     const int half = a.rotary / 2;
     for (int idx = threadIdx.x; idx < (group + 1) * half; idx += blockDim.x) {
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         row[i] = x0 * c - x1 * s;
         row[i + half] = x0 * s + x1 * c;
     }
-    __syncthreads();
+    lds_barrier();
     if (chunk == nchunks - 1) {  // this chunk holds `pos`: append k/v to the caches
         for (int d = threadIdx.x; d < HD; d += blockDim.x) {
             a.keys[((size_t)pos * a.kv_heads + kvh) * HD + d] = knew[d];
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
             stv<E>(ks[tt] + E * lane, kr[i]);
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // scores and chunk-local softmax: wave w takes query heads w, w+4, ...; lane t is
     // position t0 + t (model.cpp:143-150)
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
             lstat[g] = l;
         }
     }
-    __syncthreads();  // scores done: the key tile's LDS now takes the P.V sums
+    lds_barrier();  // scores done: the key tile's LDS now takes the P.V sums
 
     // o[g] = sum_t p[g][t] v_t over this wave's positions
     float acc[kMaxGroup][E];
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g)
         if (g < group) stv<E>(acc_lds[wave][g] + E * lane, acc[g]);
-    __syncthreads();
+    lds_barrier();
     const int stride = HD + 2;
     float* part = a.partial + ((size_t)kvh * chunks_max + chunk) * group * stride;
     for (int idx = threadIdx.x; idx < group * HD; idx += blockDim.x) {
@@ -265,7 +266,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
     }
     mloc = wave_max(mloc);
     if (lane == 0) red[wave] = mloc;
-    __syncthreads();
+    lds_barrier();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float dloc = 0.f;
     for (int c = threadIdx.x; c < nchunks; c += blockDim.x) {
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
         dloc = fmaf(w, base[(size_t)c * cstride + hd + 1], dloc);
     }
     dloc = wave_sum(dloc);
-    __syncthreads();  // every weight is in wts; red is free again
+    lds_barrier();  // every weight is in wts; red is free again
     if (lane == 0) red[4 + wave] = dloc;
     float num = 0.f;
 #pragma unroll
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
             if (c0 + 4 * i < nchunks) num = fmaf(wts[c0 + 4 * i], ov[i], num);
     }
     part[wave][lane] = num;
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
         const float den = (red[4] + red[5]) + (red[6] + red[7]);
         const float o = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);

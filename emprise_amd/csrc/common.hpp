@@ -53,6 +53,28 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` holds >= 16 floats.
+// Workgroup barrier that orders LDS accesses only. __syncthreads() also carries a
+// global-memory release, which waits for every outstanding vector memory operation of
+// the wave, loads included: a kernel that has weight loads in flight would drain them
+// at the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Sum over the workgroup (red: one float per wave) with LDS-only barriers.
+__device__ __forceinline__ float block_sum_lds(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    v = wave_sum(v);
+    lds_barrier();
+    if (lane == 0) red[wave] = v;
+    lds_barrier();
+    float t = 0.f;
+    for (int i = 0; i < waves; ++i) t += red[i];
+    return t;
+}
+
 __device__ __forceinline__ float block_sum(float v, float* red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     v = wave_sum(v);
