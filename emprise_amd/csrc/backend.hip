@@ -467,10 +467,41 @@ emprise_status emprise_hip_linear_norm(emprise_hip* h, const emprise_hip_input* 
     return run_matvec(h, p, n, kMvPlain, in, nullptr, nullptr, nullptr, 0, nullptr);
 }
 
+// Batches of at least this many tokens run as a GEMM on the matrix cores; smaller ones
+// as matvecs, which read the weights once per token at full HBM speed.
+constexpr int kGemmMinBatch = 8;
+constexpr size_t kGemmScratchBytes = size_t(256) << 20;  // dequantised weight rows per GEMM pass
+
 emprise_status emprise_hip_linear_batch(emprise_hip* h, emprise_weight w, emprise_dev X, emprise_dev Y, int K) {
     if (!h || !X || !Y || K < 1) return fail(EMPRISE_EINVAL, "bad arguments");
     const Weight* wt;
     TRY(check_weights(h, 1, &w, &wt));
+    const int cols = (int)wt->cols, rows = (int)wt->rows;
+    if (K >= kGemmMinBatch && cols % 16 == 0 && X % 16 == 0) {
+        const float* A = reinterpret_cast<const float*>(X);
+        float* C = reinterpret_cast<float*>(Y);
+        const uint64_t flops_per_row = 2ull * (uint64_t)K * (uint64_t)cols;
+        if (wt->type == kF32) {
+            return traced(h, "gemm_f32", flops_per_row * rows, [&] {
+                return launch_gemm_f32(A, reinterpret_cast<const float*>(wt->dev), C, K, rows, cols, cols, cols, rows, h->stream);
+            });
+        }
+        // quantised weights: dequantise a block of rows to FP32 (exact), then multiply
+        const uint64_t block = std::max<uint64_t>(128, kGemmScratchBytes / ((uint64_t)cols * 4) / 128 * 128);
+        const uint64_t nb = std::min<uint64_t>(block, (uint64_t)rows);
+        void* wf;
+        TRY(h->get_scratch("gemm_w", nb * cols * sizeof(float), &wf));
+        for (uint64_t r0 = 0; r0 < (uint64_t)rows; r0 += nb) {
+            const uint64_t n = std::min<uint64_t>(nb, rows - r0);
+            TRY(traced(h, "dequant_rows", n * wt->bytes / rows + n * cols * 4, [&] {
+                return launch_dequant_rows(wt->dev, wt->type, cols, r0, n, static_cast<float*>(wf), h->stream);
+            }));
+            TRY(traced(h, "gemm_f32", flops_per_row * n, [&] {
+                return launch_gemm_f32(A, static_cast<const float*>(wf), C + r0, K, (int)n, cols, cols, cols, rows, h->stream);
+            }));
+        }
+        return EMPRISE_OK;
+    }
     for (int k = 0; k < K; ++k) {
         Proj p{wt, reinterpret_cast<float*>(Y) + (size_t)k * wt->rows};
         TRY(run_matvec(h, &p, 1, kMvPlain, nullptr, reinterpret_cast<const float*>(X) + (size_t)k * wt->cols, nullptr,

@@ -72,6 +72,11 @@ hipError_t launch_matvec_stream(uint32_t type, bool q8, const MvArgs& a, hipStre
 hipError_t launch_dequant_rows(const uint8_t* w, uint32_t type, int cols, uint64_t row0, uint64_t n, float* out,
                                hipStream_t stream);
 
+// Y[M][N] (row stride ldc) = A[M][K] (lda) . B[N][K]^T (ldb), FP32 on the matrix cores.
+// K must be a multiple of 16; lda and ldb multiples of 4 (16-byte rows).
+hipError_t launch_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
+                           hipStream_t stream);
+
 // ---- Gated DeltaNet ----
 struct GdnArgs {
     int key_heads, value_heads, state_dim, conv_width;

@@ -64,6 +64,33 @@ def test_linear_lm_head(backend, wtype):
     assert np.all(np.isfinite(y))
 
 
+@pytest.mark.parametrize("wtype,K,rows,cols", [(Q6_K, 3, 64, 512), (Q6_K, 37, 300, 512), (Q4_K, 130, 257, 4096),
+                                               (F32, 9, 33, 256), (Q6_K, 64, 512, 12288), (F16, 20, 40, 1536)])
+def test_linear_batch(backend, wtype, K, rows, cols):
+    """Backend::linear_batch (backend.hpp:20-24): Y[k] = W X[k]. From 8 tokens up it runs
+    as an FP32 GEMM on the matrix cores (exact dequantised weights, FP32 products);
+    every token must match the CPU matvec, and the single-token projection, to the
+    per-op bar (batched == sequential, reference tests/core.cpp:149-164)."""
+    rng = np.random.default_rng(K * 131 + rows + cols + wtype)
+    raw = matrix(rng, wtype, rows, cols)
+    X = rng.standard_normal((K, cols)).astype(np.float32)
+    w = backend.upload_weight(wtype, cols, rows, raw)
+    xd, yd = backend.to_device(X), backend.alloc(K * rows * 4)
+    backend.linear_batch(w, xd, yd, K)
+    Y = backend.download(yd, (K, rows))
+    x1, y1 = backend.alloc(cols * 4), backend.alloc(rows * 4)
+    for k in range(K):
+        ref = oracle.matvec(wtype, raw, X[k], rows)
+        _close(Y[k], ref)
+        if k in (0, K - 1):
+            backend.upload(x1, X[k])
+            backend.linear(w, x1, y1)
+            _close(Y[k], backend.download(y1, rows))
+    for b in (xd, yd, x1, y1):
+        backend.free(b)
+    backend.weight_free(w)
+
+
 @pytest.mark.parametrize("wtype,rows,cols", [(Q6_K, 300, 4096), (Q4_K, 300, 4096), (Q6_K, 5, 1536), (Q4_K, 7, 512),
                                              (F16, 9, 512), (BF16, 9, 512), (F32, 9, 256)])
 def test_dequantize_bit_exact(backend, wtype, rows, cols):
