@@ -83,13 +83,16 @@ def hip_lib() -> ctypes.CDLL:
         "emprise_hip_linear": (st, [vp, u64, u64, u64]),
         "emprise_hip_linear_many": (st, [vp, i32, P(u64), u64, P(u64)]),
         "emprise_hip_linear_batch": (st, [vp, u64, u64, u64, i32]),
+        "emprise_hip_linear_batch_strided": (st, [vp, u64, u64, u64, u64, u64, i32]),
         "emprise_hip_linear_norm": (st, [vp, vp, i32, P(u64), P(u64)]),
         "emprise_hip_feed_forward": (st, [vp, vp, u64, u64, u64, u64, u64]),
         "emprise_hip_ffn_gate_up": (st, [vp, vp, u64, u64, u64, u64]),
         "emprise_hip_rmsnorm": (st, [vp, u64, u64, u64, i32, f32]),
+        "emprise_hip_rmsnorm_rows": (st, [vp, u64, u64, u64, i32, i32, f32]),
         "emprise_hip_add": (st, [vp, u64, u64, i32]),
         "emprise_hip_swiglu": (st, [vp, u64, u64, i32]),
         "emprise_hip_embed": (st, [vp, u64, u64, u64]),
+        "emprise_hip_embed_rows": (st, [vp, u64, u64, i32, u64]),
         "emprise_hip_argmax": (st, [vp, u64, i32, u64]),
         "emprise_hip_quantize_q8": (st, [vp, u64, i32, u64, u64]),
         "emprise_hip_delta_net": (st, [vp, vp]),
@@ -257,6 +260,9 @@ class HipBackend:
     def linear_batch(self, w: int, X: int, Y: int, K: int):
         self._check(self.lib.emprise_hip_linear_batch(self.h, w, X, Y, K))
 
+    def linear_batch_strided(self, w: int, X: int, ldx: int, Y: int, ldy: int, K: int):
+        self._check(self.lib.emprise_hip_linear_batch_strided(self.h, w, X, ldx, Y, ldy, K))
+
     def feed_forward(self, gate: int, up: int, down: int, x: int, y: int, inp: Input | None = None):
         self._check(self.lib.emprise_hip_feed_forward(self.h, ctypes.byref(inp) if inp else None, x, gate, up, down, y))
 
@@ -266,6 +272,9 @@ class HipBackend:
     def rmsnorm(self, x: int, w: int, out: int, n: int, eps: float):
         self._check(self.lib.emprise_hip_rmsnorm(self.h, x, w, out, n, eps))
 
+    def rmsnorm_rows(self, x: int, w: int, out: int, n: int, rows: int, eps: float):
+        self._check(self.lib.emprise_hip_rmsnorm_rows(self.h, x, w, out, n, rows, eps))
+
     def add(self, x: int, y: int, n: int):
         self._check(self.lib.emprise_hip_add(self.h, x, y, n))
 
@@ -274,6 +283,9 @@ class HipBackend:
 
     def embed(self, w: int, token: int, out: int):
         self._check(self.lib.emprise_hip_embed(self.h, w, token, out))
+
+    def embed_rows(self, w: int, tokens: int, count: int, out: int):
+        self._check(self.lib.emprise_hip_embed_rows(self.h, w, tokens, count, out))
 
     def argmax(self, logits: int, n: int, index: int):
         self._check(self.lib.emprise_hip_argmax(self.h, logits, n, index))
@@ -336,7 +348,7 @@ def gpu_available() -> bool:
 class ModelOptions(ctypes.Structure):
     _fields_ = [("path", ctypes.c_char_p), ("context", ctypes.c_size_t), ("device", ctypes.c_int),
                 ("weight_vram_budget", ctypes.c_uint64), ("quantize_activations", ctypes.c_int),
-                ("fused", ctypes.c_int), ("graph", ctypes.c_int)]
+                ("fused", ctypes.c_int), ("graph", ctypes.c_int), ("batch_prefill", ctypes.c_int)]
 
 
 class ModelInfo(ctypes.Structure):
@@ -440,10 +452,13 @@ class Model:
     """The C++ host's qwen35 model on the MI355X (Model::Model / evaluate / generate)."""
 
     def __init__(self, path, context: int = 4096, device: int = 0, vram_budget: int = 0, fast_q8: bool = False,
-                 fused: bool = True, graph: bool = True):
+                 fused: bool = True, graph: bool = True, batch_prefill: int = 0):
+        """batch_prefill: prompts with at least this many tokens before the last prefill
+        in batches (GEMM projections); 0 = the library default (64), -1 = never."""
         lib = host_lib()
         self._path = str(path).encode()
-        o = ModelOptions(self._path, context, device, vram_budget, int(fast_q8), int(fused), int(graph))
+        o = ModelOptions(self._path, context, device, vram_budget, int(fast_q8), int(fused), int(graph),
+                         int(batch_prefill))
         m = ctypes.c_void_p()
         _host_check(lib.emprise_model_open(ctypes.byref(o), ctypes.byref(m)))
         self.m = m

@@ -473,17 +473,27 @@ constexpr int kGemmMinBatch = 8;
 constexpr size_t kGemmScratchBytes = size_t(256) << 20;  // dequantised weight rows per GEMM pass
 
 emprise_status emprise_hip_linear_batch(emprise_hip* h, emprise_weight w, emprise_dev X, emprise_dev Y, int K) {
+    const Weight* wt = h ? h->weight(w) : nullptr;
+    if (!wt) return fail(EMPRISE_EINVAL, "bad arguments");
+    return emprise_hip_linear_batch_strided(h, w, X, wt->cols, Y, wt->rows, K);
+}
+
+emprise_status emprise_hip_linear_batch_strided(emprise_hip* h, emprise_weight w, emprise_dev X, uint64_t ldx,
+                                                emprise_dev Y, uint64_t ldy, int K) {
     if (!h || !X || !Y || K < 1) return fail(EMPRISE_EINVAL, "bad arguments");
     const Weight* wt;
     TRY(check_weights(h, 1, &w, &wt));
     const int cols = (int)wt->cols, rows = (int)wt->rows;
-    if (K >= kGemmMinBatch && cols % 16 == 0 && X % 16 == 0) {
+    if (ldx < wt->cols || ldy < wt->rows || ldx > (1u << 30) || ldy > (1u << 30))
+        return fail(EMPRISE_EINVAL, "row strides shorter than the matrix");
+    if (K >= kGemmMinBatch && cols % 16 == 0 && X % 16 == 0 && ldx % 4 == 0) {
         const float* A = reinterpret_cast<const float*>(X);
         float* C = reinterpret_cast<float*>(Y);
         const uint64_t flops_per_row = 2ull * (uint64_t)K * (uint64_t)cols;
         if (wt->type == kF32) {
             return traced(h, "gemm_f32", flops_per_row * rows, [&] {
-                return launch_gemm_f32(A, reinterpret_cast<const float*>(wt->dev), C, K, rows, cols, cols, cols, rows, h->stream);
+                return launch_gemm_f32(A, reinterpret_cast<const float*>(wt->dev), C, K, rows, cols, (int)ldx, cols,
+                                       (int)ldy, h->stream);
             });
         }
         // quantised weights: dequantise a block of rows to FP32 (exact), then multiply
@@ -497,14 +507,15 @@ emprise_status emprise_hip_linear_batch(emprise_hip* h, emprise_weight w, empris
                 return launch_dequant_rows(wt->dev, wt->type, cols, r0, n, static_cast<float*>(wf), h->stream);
             }));
             TRY(traced(h, "gemm_f32", flops_per_row * n, [&] {
-                return launch_gemm_f32(A, static_cast<const float*>(wf), C + r0, K, (int)n, cols, cols, cols, rows, h->stream);
+                return launch_gemm_f32(A, static_cast<const float*>(wf), C + r0, K, (int)n, cols, (int)ldx, cols,
+                                       (int)ldy, h->stream);
             }));
         }
         return EMPRISE_OK;
     }
     for (int k = 0; k < K; ++k) {
-        Proj p{wt, reinterpret_cast<float*>(Y) + (size_t)k * wt->rows};
-        TRY(run_matvec(h, &p, 1, kMvPlain, nullptr, reinterpret_cast<const float*>(X) + (size_t)k * wt->cols, nullptr,
+        Proj p{wt, reinterpret_cast<float*>(Y) + (size_t)k * ldy};
+        TRY(run_matvec(h, &p, 1, kMvPlain, nullptr, reinterpret_cast<const float*>(X) + (size_t)k * ldx, nullptr,
                        nullptr, 0, nullptr));
     }
     return EMPRISE_OK;
@@ -547,6 +558,27 @@ emprise_status emprise_hip_rmsnorm(emprise_hip* h, emprise_dev x, emprise_weight
     if (wt->type != kF32 || wt->rows * wt->cols != (uint64_t)n) return fail(EMPRISE_EINVAL, "RMS normalization dimensions");
     return traced(h, "rmsnorm", (uint64_t)n * 12, [&] { return launch_rmsnorm(reinterpret_cast<const float*>(x), reinterpret_cast<const float*>(wt->dev),
                                    reinterpret_cast<float*>(out), n, eps, h->stream); });
+}
+
+emprise_status emprise_hip_rmsnorm_rows(emprise_hip* h, emprise_dev x, emprise_weight w, emprise_dev out, int n,
+                                       int rows, float eps) {
+    const Weight* wt = h ? h->weight(w) : nullptr;
+    if (!wt || !x || !out || n < 1 || rows < 1) return fail(EMPRISE_EINVAL, "bad arguments");
+    if (wt->type != kF32 || wt->rows * wt->cols != (uint64_t)n) return fail(EMPRISE_EINVAL, "RMS normalization dimensions");
+    return traced(h, "rmsnorm", (uint64_t)n * rows * 8 + (uint64_t)n * 4, [&] {
+        return launch_rmsnorm_rows(reinterpret_cast<const float*>(x), reinterpret_cast<const float*>(wt->dev),
+                                   reinterpret_cast<float*>(out), n, rows, eps, h->stream);
+    });
+}
+
+emprise_status emprise_hip_embed_rows(emprise_hip* h, emprise_weight embedding, emprise_dev tokens, int count,
+                                      emprise_dev out) {
+    const Weight* w = h ? h->weight(embedding) : nullptr;
+    if (!w || !tokens || !out || count < 1 || count > 65535) return fail(EMPRISE_EINVAL, "bad arguments");
+    return traced(h, "embed", (w->bytes / w->rows + w->cols * 4) * count, [&] {
+        return launch_embed_rows(w->dev, w->type, (int)w->cols, (int)w->rows, reinterpret_cast<const int*>(tokens),
+                                 count, reinterpret_cast<float*>(out), h->stream);
+    });
 }
 
 emprise_status emprise_hip_add(emprise_hip* h, emprise_dev x, emprise_dev y, int n) {

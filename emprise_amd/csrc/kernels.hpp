@@ -117,10 +117,14 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_fill(float* dst, float value, size_t n, hipStream_t stream);
 hipError_t launch_fill_u64(unsigned long long* dst, unsigned long long value, size_t n, hipStream_t stream);
 hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t stream);
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int n, int rows, float eps,
+                               hipStream_t stream);
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream);
 hipError_t launch_swiglu(float* gate, const float* up, int n, hipStream_t stream);
 hipError_t launch_embed(const uint8_t* w, uint32_t type, int cols, int rows, const int* token, float* out,
                         hipStream_t stream);
+hipError_t launch_embed_rows(const uint8_t* w, uint32_t type, int cols, int rows, const int* tokens, int count,
+                             float* out, hipStream_t stream);
 hipError_t launch_argmax(const float* logits, int n, unsigned long long* key, int* index, hipStream_t stream);
 hipError_t launch_argmax_finish(const unsigned long long* key, int* index, hipStream_t stream);
 hipError_t launch_quantize_q8(const float* x, int cols, int8_t* q, float* scales, hipStream_t stream);

@@ -17,9 +17,12 @@ __global__ void fill_u64_kernel(unsigned long long* dst, unsigned long long valu
         dst[i] = value;
 }
 
-// rmsnorm_kernel (cuda.cpp:533-542) / rms (model.cpp:19-25): out = x * (scale * w)
+// rmsnorm_kernel (cuda.cpp:533-542) / rms (model.cpp:19-25): out = x * (scale * w);
+// workgroup r normalises row r of x (rows of n floats)
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const float* w, float* out, int n, float eps) {
     __shared__ float red[16];
+    x += (size_t)blockIdx.x * n;
+    out += (size_t)blockIdx.x * n;
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
     const float total = block_sum(ss, red);
@@ -38,8 +41,10 @@ __global__ void swiglu_kernel(float* gate, const float* up, int n) {
     if (i < n) gate[i] = siluf_(gate[i]) * up[i];
 }
 
+// row blockIdx.y of out = embedding row token[blockIdx.y]
 __global__ void embed_kernel(const uint8_t* w, uint32_t type, int cols, int rows, const int* token, float* out) {
-    const int t = *token;
+    const int t = token[blockIdx.y];
+    out += (size_t)blockIdx.y * cols;
     if (t < 0 || t >= rows) return;  // the host validates ids before they reach the device
     for (int k = blockIdx.x * blockDim.x + threadIdx.x; k < cols; k += gridDim.x * blockDim.x)
         out[k] = decode_element(w, type, cols, (uint64_t)t, k);
@@ -117,6 +122,12 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n, flo
     launch_kernel(rmsnorm_kernel, dim3(1), dim3(1024), 0, stream, x, w, out, n, eps);
     return hipGetLastError();
 }
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int n, int rows, float eps,
+                               hipStream_t stream) {
+    if (rows < 1) return hipErrorInvalidValue;
+    launch_kernel(rmsnorm_kernel, dim3(rows), dim3(1024), 0, stream, x, w, out, n, eps);
+    return hipGetLastError();
+}
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream) {
     launch_kernel(add_kernel, dim3(grid_for((size_t)n, 256, 1u << 20)), dim3(256), 0, stream, x, y, n);
     return hipGetLastError();
@@ -129,6 +140,13 @@ hipError_t launch_embed(const uint8_t* w, uint32_t type, int cols, int rows, con
                         hipStream_t stream) {
     launch_kernel(embed_kernel, dim3(grid_for((size_t)cols, 256, 64)), dim3(256), 0, stream, w, type, cols, rows,
                        token, out);
+    return hipGetLastError();
+}
+hipError_t launch_embed_rows(const uint8_t* w, uint32_t type, int cols, int rows, const int* tokens, int count,
+                             float* out, hipStream_t stream) {
+    if (count < 1 || count > 65535) return hipErrorInvalidValue;
+    launch_kernel(embed_kernel, dim3(grid_for((size_t)cols, 256, 64), count), dim3(256), 0, stream, w, type, cols,
+                  rows, tokens, out);
     return hipGetLastError();
 }
 hipError_t launch_argmax(const float* logits, int n, unsigned long long*, int* index, hipStream_t stream) {

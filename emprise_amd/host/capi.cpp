@@ -61,6 +61,7 @@ emprise_status emprise_model_open(const emprise_model_options* o, emprise_model*
         opt.quantize_activations = o->quantize_activations != 0;
         opt.fused = o->fused != 0;
         opt.graph = o->graph != 0;
+        opt.batch_prefill_min = o->batch_prefill < 0 ? 0 : o->batch_prefill == 0 ? 64 : static_cast<size_t>(o->batch_prefill);
         auto m = std::make_unique<emprise_model>();
         m->model = std::make_unique<emprise::Model>(opt);
         m->name = m->model->backend_name();

@@ -63,6 +63,17 @@ public:
         hip_check(emprise_hip_attention(h_, &p, qkv, out), "attention");
     }
     void dev_embed(emprise_weight w, emprise_dev token, emprise_dev out) { hip_check(emprise_hip_embed(h_, w, token, out), "embed"); }
+    void dev_embed_rows(emprise_weight w, emprise_dev tokens, int count, emprise_dev out) {
+        hip_check(emprise_hip_embed_rows(h_, w, tokens, count, out), "embed_rows");
+    }
+    void dev_rmsnorm_rows(emprise_dev x, emprise_weight w, emprise_dev out, int n, int rows, float eps) {
+        hip_check(emprise_hip_rmsnorm_rows(h_, x, w, out, n, rows, eps), "rmsnorm_rows");
+    }
+    void dev_linear_batch(emprise_weight w, emprise_dev x, uint64_t ldx, emprise_dev y, uint64_t ldy, int k) {
+        hip_check(emprise_hip_linear_batch_strided(h_, w, x, ldx, y, ldy, k), "linear_batch");
+    }
+    void dev_swiglu(emprise_dev gate, emprise_dev up, int n) { hip_check(emprise_hip_swiglu(h_, gate, up, n), "swiglu"); }
+    void dev_delta_net(const emprise_hip_delta_net_params& p) { hip_check(emprise_hip_delta_net(h_, &p), "delta_net"); }
     void dev_argmax(emprise_dev logits, int n, emprise_dev index) { hip_check(emprise_hip_argmax(h_, logits, n, index), "argmax"); }
     void sync() { hip_check(emprise_hip_sync(h_), "sync"); }
     void graph_begin() { hip_check(emprise_hip_graph_begin(h_), "graph_begin"); }

@@ -349,6 +349,104 @@ std::vector<float> Model::last_hidden() {
     return h;
 }
 
+// Positions [0, count) of the prompt at dev_prompt_, in chunks of up to kPrefillChunk
+// tokens: every projection runs once per chunk as a GEMM on the matrix cores (the
+// reference batches 4 positions, model.cpp:355-366; here the whole chunk), the RMSNorms,
+// residual adds and SwiGLU run over all rows at once, and the position-by-position
+// parts -- the GDN conv + state update and attention, which read the state the
+// previous position left -- run per position on the decode kernels. Op order and
+// arithmetic are those of the unfused decode step.
+void Model::prefill_batched(size_t count) {
+    constexpr size_t kPrefillChunk = 2048;
+    HipBackend& b = *backend_;
+    const emprise_model_info& d = info_;
+    const uint64_t H = d.hidden, kd = uint64_t(d.key_heads) * d.state_dim, vd = uint64_t(d.value_heads) * d.state_dim;
+    const uint64_t ch = 2 * kd + vd, vh = d.value_heads, F = d.ffn;
+    const uint64_t qd = uint64_t(d.heads) * d.head_dim * 2, kvd = uint64_t(d.kv_heads) * d.head_dim,
+                   ao = uint64_t(d.heads) * d.head_dim;
+    const uint64_t wa = std::max({ch + vd + 2 * vh, qd + 2 * kvd, F}), wb = std::max({vd, ao, F});
+    const size_t rows = std::min(count, kPrefillChunk);
+    if (pf_rows_ < rows) {
+        for (emprise_dev* p : {&pf_x_, &pf_xn_, &pf_a_, &pf_b_, &pf_c_, &pf_pos_})
+            if (*p) b.dev_free(*p), *p = 0;
+        pf_x_ = b.dev_alloc(rows * H * 4);
+        pf_xn_ = b.dev_alloc(rows * H * 4);
+        pf_a_ = b.dev_alloc(rows * wa * 4);
+        pf_b_ = b.dev_alloc(rows * wb * 4);
+        pf_c_ = b.dev_alloc(rows * H * 4);
+        pf_pos_ = b.dev_alloc(rows * sizeof(int));
+        pf_rows_ = rows;
+    }
+    std::vector<int> pos(rows);
+    for (size_t p0 = 0; p0 < count; p0 += rows) {
+        const int T = static_cast<int>(std::min(rows, count - p0));
+        for (int t = 0; t < T; ++t) pos[t] = static_cast<int>(p0) + t;
+        b.dev_upload(pf_pos_, pos.data(), T * sizeof(int));
+        b.dev_embed_rows(embd_, dev_prompt_ + p0 * sizeof(int), T, pf_x_);
+        for (const Layer& L : layers_) {
+            b.dev_rmsnorm_rows(pf_x_, L.attn_norm, pf_xn_, static_cast<int>(H), T, d.eps);
+            if (L.recurrent) {
+                const uint64_t W = ch + vd + 2 * vh;
+                b.dev_linear_batch(L.qkv, pf_xn_, H, pf_a_, W, T);
+                b.dev_linear_batch(L.zgate, pf_xn_, H, pf_a_ + ch * 4, W, T);
+                b.dev_linear_batch(L.alpha, pf_xn_, H, pf_a_ + (ch + vd) * 4, W, T);
+                b.dev_linear_batch(L.beta, pf_xn_, H, pf_a_ + (ch + vd + vh) * 4, W, T);
+                emprise_hip_delta_net_params p{};
+                p.key_heads = d.key_heads;
+                p.value_heads = d.value_heads;
+                p.state_dim = d.state_dim;
+                p.conv_width = d.conv_width;
+                p.eps = d.eps;
+                p.conv = L.conv;
+                p.ssm_a = L.ssm_a;
+                p.dt = L.dt;
+                p.norm = L.ssm_norm;
+                p.conv_state = L.conv_state;
+                p.rec_state = L.rec_state;
+                for (int t = 0; t < T; ++t) {
+                    const emprise_dev row = pf_a_ + uint64_t(t) * W * 4;
+                    p.qkv = row;
+                    p.gate = row + ch * 4;
+                    p.alpha = row + (ch + vd) * 4;
+                    p.beta = row + (ch + vd + vh) * 4;
+                    p.out = pf_b_ + uint64_t(t) * vd * 4;
+                    b.dev_delta_net(p);
+                }
+                b.dev_linear_batch(L.out, pf_b_, vd, pf_c_, H, T);
+            } else {
+                const uint64_t W = qd + 2 * kvd;
+                b.dev_linear_batch(L.q, pf_xn_, H, pf_a_, W, T);
+                b.dev_linear_batch(L.k, pf_xn_, H, pf_a_ + qd * 4, W, T);
+                b.dev_linear_batch(L.v, pf_xn_, H, pf_a_ + (qd + kvd) * 4, W, T);
+                emprise_hip_attention_params p{};
+                p.heads = d.heads;
+                p.kv_heads = d.kv_heads;
+                p.head_dim = d.head_dim;
+                p.rotary = d.rotary;
+                p.context = static_cast<int>(opt_.context);
+                p.eps = d.eps;
+                p.rope_base = d.rope_base;
+                p.q_norm = L.q_norm;
+                p.k_norm = L.k_norm;
+                p.keys = L.keys;
+                p.values = L.values;
+                for (int t = 0; t < T; ++t) {
+                    p.position = pf_pos_ + uint64_t(t) * sizeof(int);
+                    b.dev_attention(p, pf_a_ + uint64_t(t) * W * 4, pf_b_ + uint64_t(t) * ao * 4);
+                }
+                b.dev_linear_batch(L.o, pf_b_, ao, pf_c_, H, T);
+            }
+            b.dev_add(pf_x_, pf_c_, static_cast<int>(T * H));
+            b.dev_rmsnorm_rows(pf_x_, L.post_norm, pf_xn_, static_cast<int>(H), T, d.eps);
+            b.dev_linear_batch(L.gate, pf_xn_, H, pf_a_, F, T);
+            b.dev_linear_batch(L.up, pf_xn_, H, pf_b_, F, T);
+            b.dev_swiglu(pf_a_, pf_b_, static_cast<int>(T * F));
+            b.dev_linear_batch(L.down, pf_a_, F, pf_c_, H, T);
+            b.dev_add(pf_x_, pf_c_, static_cast<int>(T * H));
+        }
+    }
+}
+
 std::vector<int> Model::generate(const std::vector<int>& prompt, size_t count, std::vector<double>* arrivals) {
     if (prompt.empty()) throw std::invalid_argument("Empty prompt");
     if (prompt.size() > opt_.context || count > opt_.context - prompt.size())
@@ -359,12 +457,17 @@ std::vector<int> Model::generate(const std::vector<int>& prompt, size_t count, s
     if (!count) return {};
     const int n = static_cast<int>(prompt.size());
     backend_->dev_upload(dev_prompt_, prompt.data(), prompt.size() * sizeof(int));
-    set_state(0, prompt[0], n);
     backend_->event(0);
     // prefill: every prompt position but the last skips the output head
-    for (int i = 0; i + 1 < n; ++i) {
-        if (opt_.graph) backend_->graph_launch(step_graph(false));
-        else enqueue_step(false);
+    if (opt_.batch_prefill_min && static_cast<size_t>(n - 1) >= opt_.batch_prefill_min) {
+        prefill_batched(static_cast<size_t>(n - 1));
+        set_state(n - 1, prompt[static_cast<size_t>(n - 1)], n);
+    } else {
+        set_state(0, prompt[0], n);
+        for (int i = 0; i + 1 < n; ++i) {
+            if (opt_.graph) backend_->graph_launch(step_graph(false));
+            else enqueue_step(false);
+        }
     }
     // then count steps with the output head: the first one reads the last prompt
     // token, each later one the previous greedy pick (model.cpp:497-502). The reference

@@ -22,6 +22,8 @@ struct ModelOptions {
     bool quantize_activations = false;
     bool fused = true;
     bool graph = true;
+    // prompts of at least this many tokens prefill in batches (GEMM projections); 0 = never
+    size_t batch_prefill_min = 64;
 };
 
 class Model {
@@ -51,6 +53,8 @@ private:
     emprise_weight upload(const std::string& name, uint64_t cols, uint64_t rows);
     emprise_weight upload_vector(const std::string& name, uint64_t n);
     void enqueue_step(bool logits);  // one position, reading token/position from dev_state_
+    // positions [0, count) of `tokens` (already on the device at dev_prompt_) in batches
+    void prefill_batched(size_t count);
     void set_state(int position, int token, int prompt_len);
     emprise_graph step_graph(bool logits);
 
@@ -65,6 +69,9 @@ private:
     int last_x_ = 0;  // residual buffer holding the stream after the last step
     size_t position_ = 0;
     emprise_graph graph_full_ = 0, graph_prefill_ = 0;
+    // batched prefill buffers, sized for pf_rows_ tokens on first use
+    size_t pf_rows_ = 0;
+    emprise_dev pf_x_ = 0, pf_xn_ = 0, pf_a_ = 0, pf_b_ = 0, pf_c_ = 0, pf_d_ = 0, pf_pos_ = 0;
     bool have_graph_full_ = false, have_graph_prefill_ = false;
 };
 

@@ -106,6 +106,12 @@ emprise_status emprise_hip_linear_many(emprise_hip* h, int n, const emprise_weig
 /* Backend::linear_batch (backend.hpp:23-24), linear_q6_f32_batch (cuda.cpp:350-413):
  * Y[k] = W X[k] for k < K; X is K rows of cols floats, Y K rows of rows floats. */
 emprise_status emprise_hip_linear_batch(emprise_hip* h, emprise_weight w, emprise_dev X, emprise_dev Y, int K);
+/* linear_batch with row strides (floats): X[k] at X + k*ldx, Y[k] at Y + k*ldy, so one
+ * call can write its output into a slice of wider rows (e.g. the q|k|v rows that the
+ * attention op reads). Batched prefill support; no reference counterpart (the
+ * reference prefills in chunks of 4 positions, model.cpp:355-366). */
+emprise_status emprise_hip_linear_batch_strided(emprise_hip* h, emprise_weight w, emprise_dev X, uint64_t ldx,
+                                                emprise_dev Y, uint64_t ldy, int K);
 
 /* Input transform fused into a projection's prologue. It stands for the reference's
  * dev_add + dev_rmsnorm pair in front of every projection group (model.cpp:429,
@@ -137,6 +143,9 @@ emprise_status emprise_hip_ffn_gate_up(emprise_hip* h, const emprise_hip_input* 
 /* ---- small ops ----------------------------------------------------------------------- */
 /* Backend::dev_rmsnorm (backend.hpp:64), rmsnorm_kernel cuda.cpp:533-542. */
 emprise_status emprise_hip_rmsnorm(emprise_hip* h, emprise_dev x, emprise_weight w, emprise_dev out, int n, float eps);
+/* dev_rmsnorm over `rows` consecutive rows of n floats (batched prefill). */
+emprise_status emprise_hip_rmsnorm_rows(emprise_hip* h, emprise_dev x, emprise_weight w, emprise_dev out, int n,
+                                       int rows, float eps);
 /* Backend::dev_add (backend.hpp:65), add_inplace cuda.cpp:543-546: x += y. */
 emprise_status emprise_hip_add(emprise_hip* h, emprise_dev x, emprise_dev y, int n);
 /* swiglu, cuda.cpp:560-566: gate = silu(gate) * up. */
@@ -144,6 +153,9 @@ emprise_status emprise_hip_swiglu(emprise_hip* h, emprise_dev gate, emprise_dev 
 /* Model::Impl::embed (model.cpp:367-375) on device: out = dequantised row `*token` of
  * the embedding. token is a device int32 (graph-replayable). */
 emprise_status emprise_hip_embed(emprise_hip* h, emprise_weight embedding, emprise_dev token, emprise_dev out);
+/* embed for `count` device token ids (int32): out[i] = dequantised row tokens[i]. */
+emprise_status emprise_hip_embed_rows(emprise_hip* h, emprise_weight embedding, emprise_dev tokens, int count,
+                                      emprise_dev out);
 /* Greedy pick, model.cpp:499 (std::max_element: the first maximum wins): writes the
  * int32 index of the largest of n logits to *index (device). */
 emprise_status emprise_hip_argmax(emprise_hip* h, emprise_dev logits, int n, emprise_dev index);

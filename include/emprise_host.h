@@ -30,6 +30,8 @@ typedef struct {
     int fused;                     /* 1: fused projection kernels (default); 0: one op per launch like
                                       the reference's evaluate_device (model.cpp:422-472) */
     int graph;                     /* 1: replay the decode step as a hipGraph (default) */
+    int batch_prefill;             /* prompts with at least this many tokens before the last one
+                                      prefill in batches (GEMM projections); 0 = 64, < 0 = never */
 } emprise_model_options;
 
 typedef struct emprise_model emprise_model;

@@ -91,6 +91,27 @@ def test_linear_batch(backend, wtype, K, rows, cols):
     backend.weight_free(w)
 
 
+@pytest.mark.parametrize("K", [3, 40])
+def test_linear_batch_strided(backend, K):
+    """Strided batched projection writes its rows into a slice of wider output rows."""
+    rows, cols, ldy, off = 96, 512, 300, 37
+    rng = np.random.default_rng(K)
+    raw = matrix(rng, Q6_K, rows, cols)
+    X = rng.standard_normal((K, cols + 16)).astype(np.float32)
+    w = backend.upload_weight(Q6_K, cols, rows, raw)
+    xd = backend.to_device(X)
+    Y0 = np.full((K, ldy), 7.0, np.float32)
+    yd = backend.to_device(Y0)
+    backend.linear_batch_strided(w, xd, cols + 16, yd + off * 4, ldy, K)
+    Y = backend.download(yd, (K, ldy))
+    for k in range(K):
+        _close(Y[k, off:off + rows], oracle.matvec(Q6_K, raw, X[k, :cols], rows))
+    assert np.all(Y[:, :off] == 7.0) and np.all(Y[:, off + rows:] == 7.0)
+    backend.free(xd)
+    backend.free(yd)
+    backend.weight_free(w)
+
+
 @pytest.mark.parametrize("wtype,rows,cols", [(Q6_K, 300, 4096), (Q4_K, 300, 4096), (Q6_K, 5, 1536), (Q4_K, 7, 512),
                                              (F16, 9, 512), (BF16, 9, 512), (F32, 9, 256)])
 def test_dequantize_bit_exact(backend, wtype, rows, cols):

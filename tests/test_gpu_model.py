@@ -55,6 +55,23 @@ def test_tiny_generate_matches_oracle(tiny_path, fused, graph):
     assert checked >= 8
 
 
+@pytest.mark.parametrize("n_prompt,count,context", [(200, 64, 512), (2100, 16, 4096)])
+def test_tiny_batched_prefill_matches_oracle(tiny_path, n_prompt, count, context):
+    """Batched prefill (GEMM projections over the prompt, chunks of 2048 positions, the
+    GDN and attention steps per position) leaves the recurrent states and KV caches the
+    position-by-position prefill does: greedy tokens match the CPU path."""
+    prompt = synth_prompt(7, TINY["vocab"], n_prompt)
+    ref = oracle.Model(tiny_path, context=context)
+    ref_tokens, margins = ref.generate(prompt, count)
+    with Model(tiny_path, context=context, batch_prefill=8) as m:
+        tokens, _ = m.generate(prompt, count)
+    checked = _greedy_agreement(tokens, ref_tokens, margins)
+    assert checked >= 4
+    with Model(tiny_path, context=context, batch_prefill=-1) as m:
+        seq, _ = m.generate(prompt, count)
+    assert _greedy_agreement(seq, ref_tokens, margins) >= 4
+
+
 @pytest.mark.parametrize("path_fixture", ["tiny_path", "tiny_q4m_path"])
 def test_tiny_teacher_forced_logits(request, path_fixture):
     path = request.getfixturevalue(path_fixture)

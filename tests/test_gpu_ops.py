@@ -20,6 +20,31 @@ def _close(got, ref, tol=1e-4, what=""):
     assert err <= bound, f"{what} max abs err {err:.3e} > {bound:.3e}"
 
 
+def test_rmsnorm_rows_and_embed_rows(backend):
+    """Row-wise forms used by batched prefill: every row matches the one-row op."""
+    rng = np.random.default_rng(2)
+    n, rows = 1536, 37
+    x = (rng.standard_normal((rows, n)) * 2).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+    xd, wd, od = backend.to_device(x), backend.vector(w), backend.alloc(rows * n * 4)
+    backend.rmsnorm_rows(xd, wd, od, n, rows, 1e-6)
+    got = backend.download(od, (rows, n))
+    for r in range(rows):
+        _close(got[r], oracle.rms(x[r], w, 1e-6), what=f"row {r}")
+    vocab, cols = 300, 512
+    raw = matrix(rng, Q6_K, vocab, cols)
+    emb = backend.upload_weight(Q6_K, cols, vocab, raw)
+    table = oracle.dequantize(Q6_K, raw, vocab * cols).reshape(vocab, cols)
+    toks = np.array([5, 0, 299, 17, 5], np.int32)
+    td, ed = backend.to_device(toks), backend.alloc(len(toks) * cols * 4)
+    backend.embed_rows(emb, td, len(toks), ed)
+    assert np.array_equal(backend.download(ed, (len(toks), cols)), table[toks])
+    for b in (xd, od, td, ed):
+        backend.free(b)
+    backend.weight_free(emb)
+    backend.weight_free(wd)
+
+
 def test_rmsnorm_add_swiglu(backend):
     rng = np.random.default_rng(1)
     n = 4096
