@@ -125,6 +125,116 @@ def traffic_from_profiles(model: str, kernel: str):
     return None if rec is None else rec.get("bytes_per_launch")
 
 
+def _graph_time_ms(be, fn, n=20, reps=5):
+    """Mean duration of `fn`'s launches, replayed n times per graph, reps graphs."""
+    fn()
+    be.sync()
+    be.graph_begin()
+    for _ in range(n):
+        fn()
+    g = be.graph_end()
+    be.graph_launch(g)
+    be.sync()
+    be.event_record(0)
+    for _ in range(reps):
+        be.graph_launch(g)
+    be.event_record(1)
+    ms = be.event_elapsed(0, 1) / (n * reps)
+    be.graph_destroy(g)
+    return ms
+
+
+def suite(args):
+    """The benchmark spec's other configurations, one JSON line each on stdout:
+    C1 standalone matvecs (Q6_K, Q4_K, Q8 activations), C2 GDN step and attention at
+    the 9B shape, C4a batched prefill of 2048 tokens and C4b fast-q8 decode on the
+    Q4_K_M-mix model. Synthetic seeded inputs as in the tests (tests/synth.py)."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "tests"))
+    from synth import matrix
+    import emprise_amd as ea
+
+    def emit(rec):
+        print(json.dumps(rec), flush=True)
+
+    shapes = [(4096, 4096), (12288, 4096), (4096, 12288), (151936, 4096)]
+    for q8 in (False, True):
+        be = ea.HipBackend(0, quantize_activations=q8)
+        for wtype in ((ea.Q6_K,) if q8 else (ea.Q6_K, ea.Q4_K)):
+            for rows, cols in shapes:
+                rng = np.random.default_rng(rows + cols)
+                raw = matrix(rng, wtype, rows, cols)
+                w = be.upload_weight(wtype, cols, rows, raw)
+                x = be.to_device(rng.standard_normal(cols).astype(np.float32))
+                y = be.alloc(rows * 4)
+                ms = _graph_time_ms(be, lambda: be.linear(w, x, y))
+                gbs = len(raw) / (ms * 1e-3) / 1e9
+                emit({"config": "C1", "op": "matvec", "weights": "Q6_K" if wtype == ea.Q6_K else "Q4_K",
+                      "activations": "q8" if q8 else "f32", "rows": rows, "cols": cols, "bytes": len(raw),
+                      "us": round(ms * 1e3, 2), "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+                be.free(x)
+                be.free(y)
+                be.weight_free(w)
+        be.close()
+
+    be = ea.HipBackend(0)
+    rng = np.random.default_rng(2)
+    kh, vh, sd, cw = 16, 32, 128, 4
+    ch, vd = 2 * kh * sd + vh * sd, vh * sd
+    conv = be.vector((rng.standard_normal(ch * cw) * 0.3).astype(np.float32))
+    a = be.vector((-np.exp(rng.standard_normal(vh))).astype(np.float32))
+    dt = be.vector((rng.standard_normal(vh) * 0.5).astype(np.float32))
+    nw = be.vector((1 + 0.02 * rng.standard_normal(sd)).astype(np.float32))
+    bufs = [be.to_device(rng.standard_normal(n).astype(np.float32)) for n in (ch, vd, vh, vh)]
+    cs, rs, out = be.alloc(ch * cw * 4), be.alloc(vh * sd * sd * 4), be.alloc(vd * 4)
+    be.fill(cs, 0.0, ch * cw)
+    be.fill(rs, 0.0, vh * sd * sd)
+    p = ea.DeltaNetParams(kh, vh, sd, cw, 1e-6, bufs[0], bufs[1], bufs[2], bufs[3], conv, a, dt, nw, cs, rs, out)
+    ms = _graph_time_ms(be, lambda: be.delta_net(p))
+    nbytes = 2 * vh * sd * sd * 4 + 2 * ch * cw * 4 + (ch + vd + 2 * vh + vd) * 4
+    emit({"config": "C2a", "op": "gdn_step (conv1d + delta rule, 32 v-heads x 128^2 state)", "bytes": nbytes,
+          "us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+    heads, kv, hd, rot, context = 16, 4, 256, 64, 4096
+    kvd = kv * hd
+    keys = be.to_device(rng.standard_normal((context, kvd)).astype(np.float32))
+    values = be.to_device(rng.standard_normal((context, kvd)).astype(np.float32))
+    qkv = be.to_device(rng.standard_normal(heads * hd * 2 + 2 * kvd).astype(np.float32))
+    qn, kn = be.vector(np.ones(hd, np.float32)), be.vector(np.ones(hd, np.float32))
+    ao = be.alloc(heads * hd * 4)
+    for L in (512, 2048, 4096):
+        pos = be.to_device(np.array([L - 1], np.int32))
+        pa = ea.AttentionParams(heads, kv, hd, rot, context, 1e-6, 1e7, qn, kn, keys, values, pos)
+        ms = _graph_time_ms(be, lambda: be.attention(pa, qkv, ao))
+        nbytes = 8192 * L
+        emit({"config": "C2b", "op": "attention (16Q/4KV x 256, RoPE 64, gate)", "kv_len": L, "bytes": nbytes,
+              "us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+        be.free(pos)
+    be.close()
+
+    path = model_file("9b_q4km", seed=0)
+    model = ea.Model(path, context=4096)
+    info = model.info
+    prompt = ea.synth_prompt(1, info.vocab, 2049)
+    model.generate(prompt[:80], 2)
+    t0 = time.perf_counter()
+    _, arr = model.generate(prompt, 1)
+    wall = time.perf_counter() - t0
+    # weights applied per prompt token: every matrix but the output head, plus one embedding row
+    per_tok = info.token_weight_bytes
+    emit({"config": "C4a", "op": "batched prefill, Q4_K_M mix, FP32 MFMA GEMM projections",
+          "prompt_tokens": 2048, "seconds": round(arr[0], 4), "tok_per_s": round(2048 / arr[0], 1),
+          "host_wall_s": round(wall, 3), "token_weight_bytes": per_tok})
+    model.close()
+    model = ea.Model(path, context=4096, fast_q8=True)
+    model.generate(prompt[:8], 4)
+    tokens, arr = model.generate(prompt[:512], 257)
+    rate = 256 / (arr[-1] - arr[0])
+    emit({"config": "C4b", "op": "fast-q8 greedy decode, Q4_K_M mix", "tokens": 256, "tok_per_s": round(rate, 2),
+          "token_weight_bytes": info.token_weight_bytes,
+          "hbm_roofline_fraction": round(rate * info.token_weight_bytes / 1e9 / HBM_PEAK_GBS, 4)})
+    model.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -141,6 +251,8 @@ def main():
                     help="launch every kernel from the host instead of replaying the step graph (for profilers)")
     ap.add_argument("--copy-probe", type=int, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--suite", action="store_true",
+                    help="only run the other benchmark configurations (C1, C2, C4), one JSON line each")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU decode is not part of "
@@ -148,6 +260,9 @@ def main():
         sys.exit(2)
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.suite:
+        suite(args)
         return
 
     import emprise_amd as ea
