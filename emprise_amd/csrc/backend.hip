@@ -174,9 +174,18 @@ struct Proj {
     float* y;
 };
 
+// Per-head input transform of a projection (the GDN output gate): input = rms over each
+// head_dim slice of x, times norm[0..head_dim), times SiLU(gate).
+struct HeadGate {
+    const float* gate;
+    const float* norm;
+    int head_dim;
+    float eps;
+};
+
 emprise_status run_matvec(emprise_hip* h, const Proj* p, int n, int mode, const emprise_hip_input* in,
                           const float* x_plain, const float* conv_w, float* conv_state, int conv_width,
-                          unsigned long long* argmax_key) {
+                          unsigned long long* argmax_key, const HeadGate* hg = nullptr) {
     if (n < 1 || n > kMaxSeg) return fail(EMPRISE_EINVAL, "between 1 and %d projections per call", kMaxSeg);
     const uint64_t cols = p[0].w->cols;
     for (int i = 0; i < n; ++i)
@@ -224,6 +233,12 @@ emprise_status run_matvec(emprise_hip* h, const Proj* p, int n, int mode, const 
         } else {
             a.x = x_plain;
         }
+        if (hg) {
+            a.gate = hg->gate;
+            a.norm = hg->norm;
+            a.head_dim = hg->head_dim;
+            a.eps = hg->eps;
+        }
         if (first && conv_w) {
             a.conv_w = conv_w;
             a.conv_state = conv_state;
@@ -232,7 +247,8 @@ emprise_status run_matvec(emprise_hip* h, const Proj* p, int n, int mode, const 
         a.argmax = argmax_key;
         const bool q8 = h->q8 && type == kQ6K;
         // algorithmic bytes: encoded weights + the input read (x, delta, norm) + outputs
-        uint64_t bytes = cols * 4 * (1 + (a.delta ? 1 : 0) + (a.norm ? 1 : 0) + (a.x_out ? 1 : 0));
+        uint64_t bytes = cols * 4 * (1 + (a.delta ? 1 : 0) + (a.gate ? 1 : 0) + (a.x_out ? 1 : 0)) +
+                         (a.norm ? (a.gate ? (uint64_t)a.head_dim : cols) * 4 : 0);
         for (int s = 0; s < a.nseg; ++s) bytes += p[i + s].w->bytes + (uint64_t)a.seg[s].rows * 4;
         if (a.conv_w) bytes += (uint64_t)a.seg[0].rows * a.conv_width * 4 * 3;
         TRY(traced(h, matvec_name(type, q8), bytes, [&] { return launch_matvec(type, q8, a, 2048, h->stream); }));
@@ -689,8 +705,16 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
     g.norm = reinterpret_cast<const float*>(nw->dev);
     g.state = reinterpret_cast<float*>(p->rec_state);
     g.out = dn;
-    TRY(traced(h, "gdn_step", gdn_bytes(g), [&] { return launch_gdn(g, h->stream); }));
     Proj po{w[4], reinterpret_cast<float*>(y)};
+    // With a chunked out weight whose input fits one staging pass, the per-head RMSNorm x
+    // SiLU(gate) moves into the out projection's input staging, and the state update
+    // splits each head over several workgroups (no cross-wave step left in it).
+    if ((w[4]->type == kQ6K || w[4]->type == kQ4K) && vd % kChunkCols == 0 && vd <= kChunkCols) {
+        TRY(traced(h, "gdn_step", gdn_bytes(g) - (uint64_t)vd * 4, [&] { return launch_gdn_rows(g, h->stream); }));
+        const HeadGate hg{gate, g.norm, p->state_dim, p->eps};
+        return run_matvec(h, &po, 1, kMvPlain, nullptr, dn, nullptr, nullptr, 0, nullptr, &hg);
+    }
+    TRY(traced(h, "gdn_step", gdn_bytes(g), [&] { return launch_gdn(g, h->stream); }));
     return run_matvec(h, &po, 1, kMvPlain, nullptr, dn, nullptr, nullptr, 0, nullptr);
 }
 

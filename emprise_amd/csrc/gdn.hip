@@ -113,7 +113,82 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_kernel(GdnArgs a) {
     }
 }
 
+// The state update of rows [part*SD/SPLIT, (part+1)*SD/SPLIT) of value head h, with
+// workgroup blockIdx = h*SPLIT + part; each of the 8 waves owns RPW rows and writes their
+// raw outputs o[d] = S[d,:].q straight to global memory (no cross-wave step). q and k
+// are L2-normalised by every workgroup of the head (2*SD values).
+template <int E, int SPLIT>
+__global__ __launch_bounds__(kGdnWaves * 64) void gdn_rows_kernel(GdnArgs a) {
+    constexpr int SD = 64 * E, RPW = SD / SPLIT / kGdnWaves;
+    static_assert(RPW >= 1 && RPW <= 64, "rows per wave");
+    const int h = blockIdx.x / SPLIT, part = blockIdx.x - h * SPLIT, kh = h % a.key_heads;
+    const int key_dim = a.key_heads * SD;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int d0 = part * (SD / SPLIT) + wave * RPW;
+    const float* q = a.qkv + (size_t)kh * SD;
+    const float* k = a.qkv + key_dim + (size_t)kh * SD;
+    const float* v = a.qkv + 2 * (size_t)key_dim + (size_t)h * SD;
+    float* S = a.state + (size_t)h * SD * SD;
+
+    // all loads first: the wave's state rows, v of its rows (lane r holds row d0 + r),
+    // q and k
+    float s[RPW][E];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int e = 0; e < E; ++e) s[r][e] = S[(size_t)(d0 + r) * SD + lane + 64 * e];
+    const float v_lane = v[d0 + min(lane, RPW - 1)];
+    float qv[E], kv[E], qs = 0.f, ks = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        qv[e] = q[lane + 64 * e];
+        kv[e] = k[lane + 64 * e];
+        qs += qv[e] * qv[e];
+        ks += kv[e] * kv[e];
+    }
+    qs = wave_sum(qs);
+    ks = wave_sum(ks);
+    const float qscale = 1.f / sqrtf(qs + a.eps) / sqrtf((float)SD), kscale = 1.f / sqrtf(ks + a.eps);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        qv[e] *= qscale;
+        kv[e] *= kscale;
+    }
+    const float decay = expf(a.ssm_a[h] * softplusf_(a.alpha[h] + a.dt[h]));
+    const float b = sigmoidf_(a.beta[h]);
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        float mem = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            s[r][e] *= decay;
+            mem += s[r][e] * kv[e];
+        }
+        mem = wave_sum(mem);
+        const float vd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_lane), r));
+        const float delta = (vd - mem) * b;
+        float sum = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            s[r][e] += kv[e] * delta;
+            sum += s[r][e] * qv[e];
+        }
+        sum = wave_sum(sum);
+#pragma unroll
+        for (int e = 0; e < E; ++e) S[(size_t)(d0 + r) * SD + lane + 64 * e] = s[r][e];
+        if (lane == 0) a.out[(size_t)h * SD + d0 + r] = sum;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_gdn_rows(const GdnArgs& a, hipStream_t stream) {
+    const dim3 block(kGdnWaves * 64);
+    if (a.state_dim == 64) launch_kernel(gdn_rows_kernel<1, 2>, dim3(a.value_heads * 2), block, 0, stream, a);
+    else if (a.state_dim == 128) launch_kernel(gdn_rows_kernel<2, 4>, dim3(a.value_heads * 4), block, 0, stream, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
 
 hipError_t launch_delta_conv(const float* qkv, const float* conv_w, float* conv_state, float* out, int channels,
                              int conv_width, hipStream_t stream) {

@@ -54,6 +54,11 @@ struct MvArgs {
     float* x_out;
     const float* norm;
     float eps;
+    // per-head transform instead (the GDN output gate, backend.cpp:57-58): when gate is
+    // set, input = rms over each head_dim slice of x (weights norm[0..head_dim)) * SiLU(gate);
+    // delta and x_out must be null
+    const float* gate;
+    int head_dim;
     // kMvArgmax: running maximum key (value, -index), see argmax_key()
     unsigned long long* argmax;
     // causal conv1d + SiLU epilogue on segment 0 (the GDN qkv projection), or null
@@ -95,6 +100,10 @@ struct GdnArgs {
 hipError_t launch_delta_conv(const float* qkv, const float* conv_w, float* conv_state, float* out, int channels,
                              int conv_width, hipStream_t stream);
 hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream);
+// The state update alone, each value head split over several workgroups: out gets the
+// raw per-row outputs S.q (the per-head RMSNorm x SiLU(gate) is left to the consumer,
+// the output projection's input transform).
+hipError_t launch_gdn_rows(const GdnArgs& a, hipStream_t stream);
 
 // ---- attention ----
 struct AttnArgs {

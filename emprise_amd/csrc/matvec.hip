@@ -618,7 +618,7 @@ template <int NA> struct SItem {
 // the residual delta and the norm weights.
 template <int SB, bool DN> struct SInput {
     float4 x[SB];
-    float4 d[DN ? SB : 1], w[DN ? SB : 1];
+    float4 d[DN ? SB : 1], w[DN ? SB : 1];  // delta, or the gate in the per-head mode
 };
 
 template <int SB, bool DN>
@@ -628,15 +628,16 @@ __device__ __forceinline__ void sinput_issue(const MvArgs& a, SInput<SB, DN>& s)
 #pragma unroll
     for (int k = 0; k < SB; ++k) s.x[k] = x4[min((int)threadIdx.x + k * (int)blockDim.x, n4 - 1)];
     if constexpr (DN) {
-        if (a.delta) {
-            const float4* d4 = reinterpret_cast<const float4*>(a.delta);
+        if (a.delta || a.gate) {
+            const float4* d4 = reinterpret_cast<const float4*>(a.gate ? a.gate : a.delta);
 #pragma unroll
             for (int k = 0; k < SB; ++k) s.d[k] = d4[min((int)threadIdx.x + k * (int)blockDim.x, n4 - 1)];
         }
         if (a.norm) {
             const float4* w4 = reinterpret_cast<const float4*>(a.norm);
+            const int wn4 = a.gate ? a.head_dim / 4 : n4;  // per-head weights repeat every head
 #pragma unroll
-            for (int k = 0; k < SB; ++k) s.w[k] = w4[min((int)threadIdx.x + k * (int)blockDim.x, n4 - 1)];
+            for (int k = 0; k < SB; ++k) s.w[k] = w4[min((int)threadIdx.x + k * (int)blockDim.x, n4 - 1) % wn4];
         }
     }
 }
@@ -649,7 +650,22 @@ __device__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, flo
     const int n4 = a.cols / 4;
     const bool writer = a.x_out && blockIdx.x == 0;
     float4* xs4 = reinterpret_cast<float4*>(xs);
-    if constexpr (DN) {
+    if (DN && a.gate) {
+        // per-head RMSNorm x SiLU(gate): a head is head_dim/4 consecutive float4, held
+        // by as many consecutive lanes of one wave, so its sum of squares is a
+        // butterfly over those lanes
+        const int h4 = a.head_dim / 4;
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+            float ss = s.x[k].x * s.x[k].x + s.x[k].y * s.x[k].y + s.x[k].z * s.x[k].z + s.x[k].w * s.x[k].w;
+            for (int m = 1; m < h4; m <<= 1) ss += __shfl_xor(ss, m, 64);
+            const float scale = 1.f / sqrtf(ss / (float)a.head_dim + a.eps);
+            s.x[k].x = s.x[k].x * (scale * s.w[k].x) * siluf_(s.d[k].x);
+            s.x[k].y = s.x[k].y * (scale * s.w[k].y) * siluf_(s.d[k].y);
+            s.x[k].z = s.x[k].z * (scale * s.w[k].z) * siluf_(s.d[k].z);
+            s.x[k].w = s.x[k].w * (scale * s.w[k].w) * siluf_(s.d[k].w);
+        }
+    } else if constexpr (DN) {
         float ss = 0.f;
 #pragma unroll
         for (int k = 0; k < SB; ++k) {
@@ -891,6 +907,7 @@ template <int T, bool Q8, bool PAIR, bool CONV>
 hipError_t launch_stream_mode(const MvArgs& a, size_t lds, hipStream_t stream) {
     const int threads = kStreamWaves * 64, n4 = a.cols / 4;
     if (n4 <= StageMode<1>::sb * threads) return launch_stream(matvec_stream_kernel<T, Q8, PAIR, CONV, 1>, a, lds, stream);
+    if (a.gate) return hipErrorInvalidValue;  // the per-head transform stages in one pass only
     if constexpr (!CONV) {
         if (!a.delta && !a.norm && n4 <= StageMode<2>::sb * threads)
             return launch_stream(matvec_stream_kernel<T, Q8, PAIR, false, 2>, a, lds, stream);
@@ -917,6 +934,10 @@ int matvec_rows_per_group(uint32_t type, uint64_t cols, int mode, uint64_t total
 
 hipError_t launch_matvec_stream(uint32_t type, bool q8, const MvArgs& a, hipStream_t stream) {
     const size_t lds = matvec_lds_bytes(type, a.cols, q8);
+    // per-head transform: whole heads of a power-of-two number of float4 within a wave
+    if (a.gate && (a.delta || a.x_out || !a.norm || a.head_dim < 4 || a.head_dim > 256 || a.head_dim % 4 ||
+                   ((a.head_dim / 4) & (a.head_dim / 4 - 1)) || a.cols % a.head_dim))
+        return hipErrorInvalidValue;
     if (a.rows_per_group != (a.mode == kMvSwiglu ? kMvStreamPairRows : kMvStreamRows)) return hipErrorInvalidValue;
     // the conv epilogue holds an item's rows x taps in the lanes of one wave
     if (a.conv_w && (a.mode == kMvSwiglu || a.conv_width < 1 || a.conv_width * a.rows_per_group > 64))
@@ -1013,6 +1034,7 @@ hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, 
     const dim3 grid(blocks), block(256);
     const bool pair = a.mode == kMvSwiglu;
     if ((type == kQ6K || type == kQ4K) && a.cols % kChunkCols == 0) return launch_matvec_stream(type, q8, a, stream);
+    if (a.gate) return hipErrorInvalidValue;  // the per-head input transform is a streaming-kernel feature
     switch (type) {
     case kQ6K:
         if (q8) {

@@ -83,3 +83,18 @@ def decode_q6k_block(b: np.ndarray) -> np.ndarray:
         high = (int(b[128 + half * 32 + l]) >> (2 * g)) & 3
         out[i] = d * sc[i // 16] * ((low | high << 4) - 32)
     return out
+
+
+def quantize_like_reference(x):
+    """core.cpp:119-125: x' = round(x/s) * fp16(s) per 32, s = amax/127."""
+    q = np.empty_like(x)
+    for s0 in range(0, x.size, 32):
+        blk = x[s0:s0 + 32]
+        s = np.float32(np.max(np.abs(blk)) / np.float32(127))
+        if s == 0:
+            q[s0:s0 + 32] = 0
+            continue
+        r = np.round(blk / s)
+        r = np.where(np.abs(blk / s - np.trunc(blk / s)) == 0.5, np.trunc(blk / s) + np.sign(blk), r)
+        q[s0:s0 + 32] = r.astype(np.float32) * np.float32(np.float16(s))
+    return q

@@ -9,7 +9,7 @@ import pytest
 
 import oracle
 from emprise_amd import BF16, F16, F32, Q4_K, Q6_K, Input, InvalidArgument
-from synth import matrix
+from synth import quantize_like_reference, matrix
 
 pytestmark = pytest.mark.gpu
 
@@ -206,25 +206,10 @@ def test_feed_forward(backend, wtype):
         backend.weight_free(w)
 
 
-def _quantize_like_reference(x):
-    """core.cpp:119-125: x' = round(x/s) * fp16(s) per 32, s = amax/127."""
-    q = np.empty_like(x)
-    for s0 in range(0, x.size, 32):
-        blk = x[s0:s0 + 32]
-        s = np.float32(np.max(np.abs(blk)) / np.float32(127))
-        if s == 0:
-            q[s0:s0 + 32] = 0
-            continue
-        r = np.round(blk / s)
-        r = np.where(np.abs(blk / s - np.trunc(blk / s)) == 0.5, np.trunc(blk / s) + np.sign(blk), r)
-        q[s0:s0 + 32] = r.astype(np.float32) * np.float32(np.float16(s))
-    return q
-
-
 @pytest.mark.parametrize("rows,cols", [(256, 4096), (4096, 4096), (1024, 12288)])
 def test_q8_path(backend_q8, rows, cols):
     raw, x, got = _run_linear(backend_q8, Q6_K, rows, cols, seed=rows + cols)
-    ref = oracle.matvec(Q6_K, raw, _quantize_like_reference(x), rows)
+    ref = oracle.matvec(Q6_K, raw, quantize_like_reference(x), rows)
     assert np.all(np.abs(got - ref) <= 1e-3 + 1e-4 * np.abs(ref)), np.max(np.abs(got - ref))
     assert "Q8" in backend_q8.name
 

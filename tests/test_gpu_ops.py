@@ -9,7 +9,7 @@ import pytest
 import oracle
 from emprise_amd import (F32, Q4_K, Q6_K, AttentionParams, DeltaNetParams, Input, InvalidArgument,
                          RecurrentParams)
-from synth import matrix
+from synth import matrix, quantize_like_reference
 
 pytestmark = pytest.mark.gpu
 
@@ -153,11 +153,13 @@ def test_delta_net_steps(backend, kh, vh, sd, cw):
         assert np.array_equal(backend.download(conv_g, ch * cw), conv_c)  # conv history is a copy
 
 
-@pytest.mark.parametrize("wtype", [Q6_K, Q4_K])
-def test_recurrent_block(backend, wtype):
-    """dev_recurrent: fused projections + conv epilogue + scan + out projection."""
+@pytest.mark.parametrize("wtype,kh,vh,sd", [(Q6_K, 16, 32, 128), (Q4_K, 16, 32, 128), (Q6_K, 16, 64, 64)])
+def test_recurrent_block(backend, wtype, kh, vh, sd):
+    """dev_recurrent: fused projections + conv epilogue + scan + out projection. With a
+    4096-wide chunked out weight the state update runs split per head and the per-head
+    RMSNorm x SiLU(gate) runs in the out projection's input staging."""
     rng = np.random.default_rng(7)
-    H, kh, vh, sd, cw, eps = 4096, 16, 32, 128, 4, 1e-6
+    H, cw, eps = 4096, 4, 1e-6
     kd, vd = kh * sd, vh * sd
     ch = 2 * kd + vd
     prm = _gdn_inputs(rng, kh, vh, sd, cw)
@@ -180,6 +182,43 @@ def test_recurrent_block(backend, wtype):
         ref = oracle.matvec(wtype, raws["out"][2], dn, H)
         _close(backend.download(yd, H), ref, tol=2e-4, what=f"step {step}")
         _close(backend.download(rec_g, vh * sd * sd), rec_c, tol=2e-4, what=f"step {step} state")
+
+
+def test_recurrent_block_q8(backend_q8):
+    """--fast-q8 on the 9B recurrent shape: every Q6_K projection quantises its input
+    (core.cpp:119-125), the out projection after the per-head norm x gate of its staging.
+    Tolerance: the Q8 matvec bound, plus one +-1 rounding flip of a quantised dn value
+    (dn differs from the CPU's in the last bits before quantisation)."""
+    rng = np.random.default_rng(17)
+    H, kh, vh, sd, cw, eps = 4096, 16, 32, 128, 4, 1e-6
+    kd, vd = kh * sd, vh * sd
+    ch = 2 * kd + vd
+    prm = _gdn_inputs(rng, kh, vh, sd, cw)
+    raws = {"qkv": (ch, H), "gate": (vd, H), "alpha": (vh, H), "beta": (vh, H), "out": (H, vd)}
+    raws = {k: (r, c, matrix(rng, Q6_K, r, c)) for k, (r, c) in raws.items()}
+    ws = {k: backend_q8.upload_weight(Q6_K, c, r, raw) for k, (r, c, raw) in raws.items()}
+    wconv, wa, wdt, wn = (backend_q8.vector(prm[k]) for k in ("conv", "ssm_a", "dt", "norm"))
+    conv_c, rec_c = np.zeros(ch * cw, np.float32), np.zeros(vh * sd * sd, np.float32)
+    conv_g, rec_g = backend_q8.to_device(conv_c), backend_q8.to_device(rec_c)
+    p = RecurrentParams(ws["qkv"], ws["gate"], ws["alpha"], ws["beta"], ws["out"], wconv, wa, wdt, wn, kh, vh, sd,
+                        cw, eps, conv_g, rec_g)
+    xd, yd = backend_q8.alloc(H * 4), backend_q8.alloc(H * 4)
+    wout = oracle.dequantize(Q6_K, raws["out"][2], H * vd).reshape(H, vd)
+    for step in range(3):
+        x = rng.standard_normal(H).astype(np.float32)
+        backend_q8.upload(xd, x)
+        backend_q8.recurrent(p, xd, yd)
+        xq = quantize_like_reference(x)
+        proj = {k: oracle.matvec(Q6_K, raws[k][2], xq, raws[k][0]) for k in ("qkv", "gate", "alpha", "beta")}
+        dn = oracle.delta_net(kh, vh, sd, cw, eps, proj["qkv"], proj["gate"], proj["alpha"], proj["beta"],
+                              prm["conv"], prm["ssm_a"], prm["dt"], prm["norm"], conv_c, rec_c)
+        ref = oracle.matvec(Q6_K, raws["out"][2], quantize_like_reference(dn), H)
+        got = backend_q8.download(yd, H)
+        step_q = np.repeat(np.max(np.abs(dn.reshape(-1, 32)), axis=1) / 127, 32)  # one quantum per column
+        flip = np.max(np.abs(wout) * step_q[None, :], axis=1)
+        bad = np.abs(got - ref) > 1e-3 + 1e-4 * np.abs(ref) + flip
+        assert not bad.any(), (step, int(bad.sum()), float(np.max(np.abs(got - ref))))
+        _close(backend_q8.download(rec_g, vh * sd * sd), rec_c, tol=2e-4, what=f"step {step} state")
 
 
 def _attention_case(backend, heads, kv, hd, rot, L, context, seed, base=1e7, eps=1e-6):
