@@ -68,13 +68,14 @@ int main(int argc, char** argv) {
             else if (arg == "--unfused") opt.fused = 0;
             else if (arg == "--no-graph") opt.graph = 0;
             else if (arg == "--no-batch-prefill") opt.batch_prefill = -1;
+            else if (arg == "--step-program") opt.step_program = 1;
             else if (arg == "--cpu") throw std::invalid_argument("--cpu: this build runs on the MI355X backend only");
             else throw std::invalid_argument("Unknown option: " + arg);
         }
         if (model.empty())
             throw std::invalid_argument("Usage: emprise-chat --model MODEL.gguf (--prompt-ids 1,2,3 | --synthetic-prompt N "
                                         "[--seed S]) [--tokens N] [--context N] [--fast-q8] [--report FILE] [--unfused] "
-                                        "[--no-graph] [--no-batch-prefill]");
+                                        "[--no-graph] [--no-batch-prefill] [--step-program]");
         opt.path = model.c_str();
         const auto start = std::chrono::steady_clock::now();
         emprise_model* m = nullptr;

@@ -293,6 +293,8 @@ emprise_graph Model::step_graph(bool logits) {
     bool& have = logits ? have_graph_full_ : have_graph_prefill_;
     emprise_graph& g = logits ? graph_full_ : graph_prefill_;
     if (!have) {
+        const bool program = opt_.step_program && opt_.fused && step_program_ != 0;
+        hip_check(emprise_hip_set_step_program(backend_->get(), program ? 1 : 0), "step_program");
         backend_->graph_begin();
         try {
             enqueue_step(logits);
@@ -301,7 +303,26 @@ emprise_graph Model::step_graph(bool logits) {
             (void)emprise_hip_graph_end(backend_->get(), &dead);
             throw;
         }
-        g = backend_->graph_end();
+        emprise_graph rec = 0;
+        const emprise_status st = emprise_hip_graph_end(backend_->get(), &rec);
+        if (program && st == EMPRISE_EUNSUPPORTED) {
+            // a call or shape the step program cannot express: per-op graph instead
+            hip_check(emprise_hip_set_step_program(backend_->get(), 0), "step_program");
+            backend_->graph_begin();
+            try {
+                enqueue_step(logits);
+            } catch (...) {
+                emprise_graph dead = 0;
+                (void)emprise_hip_graph_end(backend_->get(), &dead);
+                throw;
+            }
+            rec = backend_->graph_end();
+            step_program_ = 0;
+        } else {
+            hip_check(st, "graph_end");
+            step_program_ = program ? 1 : 0;
+        }
+        g = rec;
         have = true;
     }
     return g;
@@ -329,6 +350,26 @@ std::vector<emprise_hip_trace_record> Model::trace_step(int token) {
     if (token < 0 || token >= info_.vocab) throw std::out_of_range("Token ID");
     set_state(static_cast<int>(position_), token, 0);
     backend_->sync();
+    const emprise_model_info& d = info_;
+    if (opt_.graph && step_program_ == 1) {
+        // the whole step is one persistent kernel (+ the one-thread finish kernel): time
+        // the replay between two events; bytes = every matrix once, the recurrent states
+        // read and written, K/V rows 0..position of the attention layers
+        const emprise_graph g = step_graph(true);
+        constexpr int kA = 65534, kB = 65535;
+        backend_->event(kA);
+        backend_->graph_launch(g);
+        backend_->event(kB);
+        const float ms = backend_->elapsed(kA, kB);
+        uint64_t bytes = d.token_weight_bytes;
+        const uint64_t kd = uint64_t(d.key_heads) * d.state_dim, vd = uint64_t(d.value_heads) * d.state_dim;
+        for (const Layer& L : layers_) {
+            if (L.recurrent) bytes += 2 * (vd * d.state_dim * 4 + (2 * kd + vd) * d.conv_width * 4);
+            else bytes += uint64_t(position_ + 1) * d.kv_heads * d.head_dim * 4 * 2;
+        }
+        ++position_;
+        return {emprise_hip_trace_record{"decode_step", bytes, ms}};
+    }
     hip_check(emprise_hip_trace_begin(backend_->get()), "trace_begin");
     enqueue_step(true);
     std::vector<emprise_hip_trace_record> rec(4096);

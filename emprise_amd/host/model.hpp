@@ -24,6 +24,8 @@ struct ModelOptions {
     bool graph = true;
     // prompts of at least this many tokens prefill in batches (GEMM projections); 0 = never
     size_t batch_prefill_min = 64;
+    // replay decode steps as one persistent kernel when the backend can record them
+    bool step_program = false;
 };
 
 class Model {
@@ -73,6 +75,12 @@ private:
     size_t pf_rows_ = 0;
     emprise_dev pf_x_ = 0, pf_xn_ = 0, pf_a_ = 0, pf_b_ = 0, pf_c_ = 0, pf_d_ = 0, pf_pos_ = 0;
     bool have_graph_full_ = false, have_graph_prefill_ = false;
+    int step_program_ = -1;  // 1: step graphs are persistent programs, 0: per-op graphs, -1: none yet
+
+public:
+    int step_program() const { return step_program_; }
+
+private:
 };
 
 }  // namespace emprise

@@ -32,6 +32,9 @@ typedef struct {
     int graph;                     /* 1: replay the decode step as a hipGraph (default) */
     int batch_prefill;             /* prompts with at least this many tokens before the last one
                                       prefill in batches (GEMM projections); 0 = 64, < 0 = never */
+    int step_program;              /* 1: the graph replays each decode step as one persistent kernel
+                                      (emprise_hip_set_step_program) when the shapes allow; 0 (default):
+                                      one graph node per op */
 } emprise_model_options;
 
 typedef struct emprise_model emprise_model;
@@ -52,6 +55,9 @@ typedef struct {
     double load_seconds;
 } emprise_model_info;
 emprise_status emprise_model_get_info(const emprise_model* m, emprise_model_info* info);
+/* 1 when decode steps run as a persistent step program, 0 when as per-op graphs (known
+ * after the first graph replay; -1 before). */
+int emprise_model_step_program(const emprise_model* m);
 
 /* Model::reset (model.cpp:479). */
 emprise_status emprise_model_reset(emprise_model* m);
