@@ -29,7 +29,7 @@ inline void launch_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream
 
 constexpr int kMaxSeg = 8;
 constexpr int kMvRows = 2;            // rows per wave iteration (unit-major rows)
-constexpr int kMvStreamRows = 2;      // rows per item of the streaming kernel (chunked rows)
+constexpr int kMvStreamRows = 1;      // rows per item of the streaming kernel (chunked rows)
 constexpr int kMvStreamPairRows = 1;  // gate/up row pairs per item of the SwiGLU variant
 
 enum MvMode : int { kMvPlain = 0, kMvSwiglu = 1, kMvArgmax = 2 };

@@ -753,8 +753,10 @@ template <int T, bool Q8> hipError_t launch_stream_kind(const MvArgs& a, size_t 
 
 }  // namespace
 
-// Rows per item of the streaming kernel: 2 rows (2 gate/up pairs), chosen by sweep
-// against 1 and 4 on the 9B shapes.
+// Rows per item of the streaming kernel: one row (one gate/up pair). Measured in the
+// 9B-shape decode (per-op graph): 1 row 510.6 tok/s, 2 rows 492.0, 4 rows 426.5 -- most
+// launches give a wave only a few items, and single-row items spread them over more
+// waves and cut the registers (66-85 VGPRs: 5-7 waves per SIMD instead of 4).
 int matvec_rows_per_group(uint32_t type, uint64_t cols, int mode, uint64_t total_rows) {
     (void)total_rows;
     if ((type == kQ6K || type == kQ4K) && cols % kChunkCols == 0)
