@@ -226,6 +226,7 @@ bool is_matrix(const Weight* w) { return w && w->rows >= 1 && w->cols >= 1; }
 struct Proj {
     const Weight* w;
     float* y;
+    bool silu = false;  // store SiLU(row) (MvArgs::silu_mask)
 };
 
 // Per-head input transform of a projection (the GDN output gate): input = rms over each
@@ -272,6 +273,7 @@ emprise_status run_matvec(emprise_hip* h, const Proj* p, int n, int mode, const 
             const Weight* w = p[i + s].w;
             a.seg[s].w = w->dev;
             a.seg[s].y = p[i + s].y;
+            if (p[i + s].silu) a.silu_mask |= 1 << s;
             a.seg[s].rows = (int)w->rows;
             a.seg[s].g0 = g;
             if (mode == kMvSwiglu && s == 1) a.seg[s].g0 = 0x7fffffff;
@@ -458,6 +460,7 @@ emprise_status rec_matvec(emprise_hip* h, const Proj* p, int n, int mode, const 
             const Weight* w = p[i + s2].w;
             m.seg[s2].w = w->dev;
             m.seg[s2].rows = (int)w->rows;
+            if (p[i + s2].silu) m.silu_mask |= 1 << s2;
             m.seg[s2].g0 = g;
             if (mode == kMvSwiglu && s2 == 1) m.seg[s2].g0 = 0x7fffffff;
             else g += (int)((w->rows + R - 1) / R);
@@ -959,7 +962,12 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
     float* alpha = gate + vd;
     float* beta = alpha + p->value_heads;
     float* dn = beta + p->value_heads;
-    Proj pr[4] = {{w[0], qkv}, {w[1], gate}, {w[2], alpha}, {w[3], beta}};
+    // With a chunked out weight whose input fits one staging pass, the per-head RMSNorm x
+    // SiLU(gate) moves into the out projection's input staging (the gate rows leave the
+    // in-projection already SiLU'd), and the state update splits each head over several
+    // workgroups (no cross-wave step left in it).
+    const bool split = (w[4]->type == kQ6K || w[4]->type == kQ4K) && vd % kChunkCols == 0 && vd <= kChunkCols;
+    Proj pr[4] = {{w[0], qkv}, {w[1], gate, split}, {w[2], alpha}, {w[3], beta}};
     // qkv first, so the conv1d + SiLU epilogue lands on its rows
     TRY(run_matvec(h, pr, 4, kMvPlain, in, reinterpret_cast<const float*>(x), reinterpret_cast<const float*>(conv->dev),
                    reinterpret_cast<float*>(p->conv_state), p->conv_width, nullptr));
@@ -980,8 +988,7 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
     g.out = dn;
     Proj po{w[4], reinterpret_cast<float*>(y)};
     if (h->recording) {
-        if ((w[4]->type != kQ6K && w[4]->type != kQ4K) || vd % kChunkCols || vd > kChunkCols)
-            return rec_unsupported(h, "recurrent output width");
+        if (!split) return rec_unsupported(h, "recurrent output width");
         StepPhase ph{};
         ph.kind = kStepGdn;
         StepGdn& sg = ph.gdn;
@@ -1001,10 +1008,7 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
         const HeadGate hg{gate, g.norm, p->state_dim, p->eps};
         return run_matvec(h, &po, 1, kMvPlain, nullptr, dn, nullptr, nullptr, 0, nullptr, &hg);
     }
-    // With a chunked out weight whose input fits one staging pass, the per-head RMSNorm x
-    // SiLU(gate) moves into the out projection's input staging, and the state update
-    // splits each head over several workgroups (no cross-wave step left in it).
-    if ((w[4]->type == kQ6K || w[4]->type == kQ4K) && vd % kChunkCols == 0 && vd <= kChunkCols) {
+    if (split) {
         TRY(traced(h, "gdn_step", gdn_bytes(g) - (uint64_t)vd * 4, [&] { return launch_gdn_rows(g, h->stream); }));
         const HeadGate hg{gate, g.norm, p->state_dim, p->eps};
         return run_matvec(h, &po, 1, kMvPlain, nullptr, dn, nullptr, nullptr, 0, nullptr, &hg);

@@ -55,10 +55,13 @@ struct MvArgs {
     const float* norm;
     float eps;
     // per-head transform instead (the GDN output gate, backend.cpp:57-58): when gate is
-    // set, input = rms over each head_dim slice of x (weights norm[0..head_dim)) * SiLU(gate);
-    // delta and x_out must be null
+    // set, input = rms over each head_dim slice of x (weights norm[0..head_dim)) * gate,
+    // where gate already holds SiLU(gate rows) (see silu_mask); delta and x_out must be null
     const float* gate;
     int head_dim;
+    // bit s: the epilogue stores SiLU(row) for segment s (the GDN gate rows, activated once
+    // by their producer instead of in every consumer workgroup)
+    int silu_mask;
     // kMvArgmax: running maximum key (value, -index), see argmax_key()
     unsigned long long* argmax;
     // causal conv1d + SiLU epilogue on segment 0 (the GDN qkv projection), or null

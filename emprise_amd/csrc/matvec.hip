@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
                     } else if (a.conv_w && s == 0) {
                         seg.y[row] = conv_step(a.conv_w, a.conv_state, a.conv_width, row, acc[r]);
                     } else {
-                        seg.y[row] = acc[r];
+                        seg.y[row] = (a.silu_mask >> s) & 1 ? siluf_(acc[r]) : acc[r];
                         if (a.mode == kMvArgmax) {
                             const unsigned long long k = argmax_key(acc[r], row);
                             best = k > best ? k : best;
@@ -490,10 +490,10 @@ __device__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, flo
             float ss = s.x[k].x * s.x[k].x + s.x[k].y * s.x[k].y + s.x[k].z * s.x[k].z + s.x[k].w * s.x[k].w;
             for (int m = 1; m < h4; m <<= 1) ss += __shfl_xor(ss, m, 64);
             const float scale = 1.f / sqrtf(ss / (float)a.head_dim + a.eps);
-            s.x[k].x = s.x[k].x * (scale * s.w[k].x) * siluf_(s.d[k].x);
-            s.x[k].y = s.x[k].y * (scale * s.w[k].y) * siluf_(s.d[k].y);
-            s.x[k].z = s.x[k].z * (scale * s.w[k].z) * siluf_(s.d[k].z);
-            s.x[k].w = s.x[k].w * (scale * s.w[k].w) * siluf_(s.d[k].w);
+            s.x[k].x = s.x[k].x * (scale * s.w[k].x) * s.d[k].x;
+            s.x[k].y = s.x[k].y * (scale * s.w[k].y) * s.d[k].y;
+            s.x[k].z = s.x[k].z * (scale * s.w[k].z) * s.d[k].z;
+            s.x[k].w = s.x[k].w * (scale * s.w[k].w) * s.d[k].w;
         }
     } else if constexpr (DN) {
         float ss = 0.f;
@@ -681,7 +681,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
                         if constexpr (PAIR) {
                             sg.y[row] = siluf_(acc[r]) * acc[(R + r) % NA];
                         } else {
-                            sg.y[row] = acc[r];
+                            sg.y[row] = (a.silu_mask >> it.seg) & 1 ? siluf_(acc[r]) : acc[r];
                             if (a.mode == kMvArgmax) {
                                 const unsigned long long k = argmax_key(acc[r], row);
                                 best = k > best ? k : best;

@@ -198,10 +198,10 @@ __device__ void step_stage(const StepMatvec& m, uint32_t tag, uint32_t base, flo
                 float q = x[k].x * x[k].x + x[k].y * x[k].y + x[k].z * x[k].z + x[k].w * x[k].w;
                 for (int s = 1; s < h4; s <<= 1) q += __shfl_xor(q, s, 64);
                 const float scale = 1.f / sqrtf(q / (float)m.head_dim + m.eps);
-                x[k].x = x[k].x * (scale * w.x) * siluf_(val(dr[k][0]));
-                x[k].y = x[k].y * (scale * w.y) * siluf_(val(dr[k][1]));
-                x[k].z = x[k].z * (scale * w.z) * siluf_(val(dr[k][2]));
-                x[k].w = x[k].w * (scale * w.w) * siluf_(val(dr[k][3]));
+                x[k].x = x[k].x * (scale * w.x) * val(dr[k][0]);
+                x[k].y = x[k].y * (scale * w.y) * val(dr[k][1]);
+                x[k].z = x[k].z * (scale * w.z) * val(dr[k][2]);
+                x[k].w = x[k].w * (scale * w.w) * val(dr[k][3]);
             }
         } else {
             const bool writer = m.x_out.p && blockIdx.x == 0;
@@ -394,7 +394,7 @@ __device__ void step_matvec(const StepMatvec& m, uint32_t tag, uint32_t base, un
                         if constexpr (PAIR) {
                             st_out(m.seg[s].y, row, siluf_(acc[r]) * acc[(R + r) % NA], tag);
                         } else {
-                            if (m.seg[s].y.p) st_out(m.seg[s].y, row, acc[r], tag);
+                            if (m.seg[s].y.p) st_out(m.seg[s].y, row, (m.silu_mask >> s) & 1 ? siluf_(acc[r]) : acc[r], tag);
                             if (m.mode == kMvArgmax) {
                                 const unsigned long long k = argmax_key(acc[r], row);
                                 best = k > best ? k : best;

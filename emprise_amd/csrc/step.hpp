@@ -48,13 +48,14 @@ struct StepMatvec {
     int cols, groups, rows_per_group, nseg;
     StepSeg seg[kMaxSeg];
     // input: v = x + delta (workgroup 0 stores v to x_out), then rms(v) * norm; or, with
-    // gate set, the per-head rms(x) * norm * SiLU(gate); or the embedding row *token of
-    // emb instead of x
+    // gate set (already SiLU'd by its producer), the per-head rms(x) * norm * gate; or the
+    // embedding row *token of emb instead of x
     StepIn x, delta, gate;
     StepOut x_out;
     const float* norm;
     float eps;
     int head_dim;
+    int silu_mask;  // bit s: segment s stores SiLU(row)
     const uint8_t* emb;
     uint32_t emb_type;
     int emb_rows;
