@@ -406,7 +406,7 @@ __device__ void sstage(const MvArgs& a, float* xs, float* usum, float* red) {
                 const float4 v = xs4[chunk_slot(u * U4 + j)];
                 s += (v.x + v.y) + (v.z + v.w);
             }
-            usum[u] = s;
+            usum[u] = stored_unit_sum<UNIT>(s);
         }
     }
 }
@@ -533,7 +533,7 @@ __device__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, flo
             t += __shfl_xor(t, 1, 64);
             t += __shfl_xor(t, 2, 64);
             if constexpr (U4 == 8) t += __shfl_xor(t, 4, 64);
-            if (i < n4 && (i & (U4 - 1)) == 0) usum[i / U4] = t;
+            if (i < n4 && (i & (U4 - 1)) == 0) usum[i / U4] = stored_unit_sum<UNIT>(t);
         }
     }
 }
@@ -681,7 +681,9 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
                         if constexpr (PAIR) {
                             sg.y[row] = siluf_(acc[r]) * acc[(R + r) % NA];
                         } else {
-                            sg.y[row] = (a.silu_mask >> it.seg) & 1 ? siluf_(acc[r]) : acc[r];
+                            float v = acc[r];
+                            if ((a.silu_mask >> it.seg) & 1) v = siluf_(v);  // wave-uniform
+                            sg.y[row] = v;
                             if (a.mode == kMvArgmax) {
                                 const unsigned long long k = argmax_key(acc[r], row);
                                 best = k > best ? k : best;

@@ -265,7 +265,7 @@ __device__ void step_stage(const StepMatvec& m, uint32_t tag, uint32_t base, flo
         t += __shfl_xor(t, 1, 64);
         t += __shfl_xor(t, 2, 64);
         if constexpr (U4 == 8) t += __shfl_xor(t, 4, 64);
-        if (i < n4 && (i & (U4 - 1)) == 0) usum[i / U4] = t;
+        if (i < n4 && (i & (U4 - 1)) == 0) usum[i / U4] = stored_unit_sum<UNIT>(t);
     }
 }
 
@@ -394,7 +394,9 @@ __device__ void step_matvec(const StepMatvec& m, uint32_t tag, uint32_t base, un
                         if constexpr (PAIR) {
                             st_out(m.seg[s].y, row, siluf_(acc[r]) * acc[(R + r) % NA], tag);
                         } else {
-                            if (m.seg[s].y.p) st_out(m.seg[s].y, row, (m.silu_mask >> s) & 1 ? siluf_(acc[r]) : acc[r], tag);
+                            float v = acc[r];
+                            if ((m.silu_mask >> s) & 1) v = siluf_(v);  // wave-uniform
+                            if (m.seg[s].y.p) st_out(m.seg[s].y, row, v, tag);
                             if (m.mode == kMvArgmax) {
                                 const unsigned long long k = argmax_key(acc[r], row);
                                 best = k > best ? k : best;

@@ -34,11 +34,11 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     return v;
 }
 
-// sum over the 16 codes of a Q6_K unit times x (codes 0..63, no zero point)
-__device__ __forceinline__ float q6_unit(uint32_t d0, uint32_t d1, uint32_t d2, const float4* x) {
+// seed + sum over the 16 codes of a Q6_K unit times x (codes 0..63, no zero point)
+__device__ __forceinline__ float q6_unit(uint32_t d0, uint32_t d1, uint32_t d2, const float4* x, float seed = 0.f) {
     const uint32_t a = opaque(d0 & 0x3F3F3F3Fu), b = opaque(d1 & 0x3F3F3F3Fu), c = opaque(d2 & 0x3F3F3F3Fu);
     const uint32_t e = opaque(((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u));
-    float s0 = dot4(a, x[0], 0.f);
+    float s0 = dot4(a, x[0], seed);
     float s1 = dot4(b, x[1], 0.f);
     s0 = dot4(c, x[2], s0);
     s1 = dot4(e, x[3], s1);
@@ -127,6 +127,12 @@ __device__ __forceinline__ void sload(SChunk<T, NA>& ch, const uint8_t* const* r
     }
 }
 
+// The per-unit input sum as the streaming kernels keep it in LDS: for Q6_K units (16
+// values) the zero-point term -32 * sum x itself (exact: a power-of-two scaling), which
+// seeds each unit's dot product; for Q4_K units (32 values) the plain sum, which the
+// dmin * m term multiplies.
+template <int UNIT> __device__ __forceinline__ float stored_unit_sum(float t) { return UNIT == 16 ? -32.f * t : t; }
+
 __device__ __forceinline__ uint32_t lane_word(const uint4& v, int j) {
     return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
 }
@@ -136,8 +142,10 @@ __device__ __forceinline__ void scompute(const SChunk<T, NA>& ch, float* acc, co
                                          int lane) {
     const float4* x4 = reinterpret_cast<const float4*>(xs) + (size_t)c * 1024 + lane;
     if constexpr (T == kQ6K) {
-        const float4 xsum = reinterpret_cast<const float4*>(usum)[c * 64 + lane];
-        const float xsv[4] = {xsum.x, xsum.y, xsum.z, xsum.w};
+        // (d*sc_u) * (sum q x - 32 sum x) per unit u: the first of the unit's two product
+        // chains starts from the stored -32 * sum x
+        const float4 off4 = reinterpret_cast<const float4*>(usum)[c * 64 + lane];
+        const float off[4] = {off4.x, off4.y, off4.z, off4.w};
         float dv[NA];
 #pragma unroll
         for (int r = 0; r < NA; ++r) dv[r] = half_bits_to_float((uint16_t)ch.d[r]);
@@ -146,12 +154,12 @@ __device__ __forceinline__ void scompute(const SChunk<T, NA>& ch, float* acc, co
             float4 xv[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) xv[i] = x4[(j * 4 + i) * 64];
-            const float off = -32.f * xsv[j];
 #pragma unroll
             for (int r = 0; r < NA; ++r) {
-                const float s = q6_unit(lane_word(ch.q[r][0], j), lane_word(ch.q[r][1], j), lane_word(ch.q[r][2], j), xv);
+                const float s = q6_unit(lane_word(ch.q[r][0], j), lane_word(ch.q[r][1], j), lane_word(ch.q[r][2], j), xv,
+                                        off[j]);
                 const float sc = (float)(int)(int8_t)(ch.sc[r] >> (8 * j));
-                acc[r] = fmaf(dv[r] * sc, s + off, acc[r]);
+                acc[r] = fmaf(dv[r] * sc, s, acc[r]);
             }
         }
     } else {
