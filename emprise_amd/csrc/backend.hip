@@ -417,6 +417,8 @@ emprise_status rec_matvec(emprise_hip* h, const Proj* p, int n, int mode, const 
                ((hg->head_dim / 4) & (hg->head_dim / 4 - 1)) || cols % hg->head_dim))
         return rec_unsupported(h, "per-head gate shape");
     if (conv_w && conv_width * kMvStreamRows > 64) return rec_unsupported(h, "conv width");
+    for (int i = 0; i < n; ++i)
+        if (p[i].silu && !conv_w) return rec_unsupported(h, "SiLU'd rows without the conv epilogue");
     // the input operands are resolved before any output of this call is registered
     StepIn x{}, delta{nullptr, -1}, gate{nullptr, -1};
     const StepEmbed* emb = nullptr;

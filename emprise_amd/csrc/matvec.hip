@@ -17,6 +17,8 @@
 // (d*sc) * (sum q*x - 32*sum x) and (d*sc)*(sum q*x) - (dmin*m)*(sum x): the same
 // products as the CPU path, grouped per unit. Only the order of FP32 additions
 // differs from the reference's sequential row sum.
+#include <mutex>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "decode.hpp"
@@ -682,7 +684,14 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
                             sg.y[row] = siluf_(acc[r]) * acc[(R + r) % NA];
                         } else {
                             float v = acc[r];
-                            if ((a.silu_mask >> it.seg) & 1) v = siluf_(v);  // wave-uniform
+                            // only the conv variant (the GDN in-projection) carries SiLU'd
+                            // segments; the empty volatile asm keeps SiLU behind the
+                            // (wave-uniform) branch instead of evaluated for every row
+                            if constexpr (CONV)
+                                if ((a.silu_mask >> it.seg) & 1) {
+                                    asm volatile("" : "+v"(v));
+                                    v = siluf_(v);
+                                }
                             sg.y[row] = v;
                             if (a.mode == kMvArgmax) {
                                 const unsigned long long k = argmax_key(acc[r], row);
@@ -711,24 +720,36 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
 }
 
 // Workgroups of a streaming launch: one full round of resident workgroups (occupancy x
-// CUs), so no wave waits for a second dispatch round.
-template <class K> int resident_blocks(K kernel, size_t lds) {
-    static int cached = 0;
-    if (!cached) {
-        int dev = 0, per_cu = 0;
-        hipDeviceProp_t prop;
-        (void)hipGetDevice(&dev);
-        (void)hipGetDeviceProperties(&prop, dev);
-        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
-                                                           kStreamWaves * 64, lds);
-        cached = (per_cu > 0 ? per_cu : 1) * prop.multiProcessorCount;
-    }
-    return cached;
+// CUs, at most two per CU), so no wave waits for a second dispatch round. Occupancy
+// differs per kernel instantiation (registers) and per LDS size, so the cache is keyed
+// by both. The cap: every workgroup stages the whole input, and a third workgroup per CU
+// (the one-row kernels have room for it) measured slower in the 9B-shape decode (508.4
+// vs 513.5 tok/s; one per CU 514.9, but slower on the in-projection and the LM head).
+int resident_blocks(const void* kernel, size_t lds) {
+    struct Entry {
+        const void* kernel;
+        size_t lds;
+        int blocks;
+    };
+    static Entry cache[64];
+    static int used = 0;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i)
+        if (cache[i].kernel == kernel && cache[i].lds == lds) return cache[i].blocks;
+    int dev = 0, per_cu = 0;
+    hipDeviceProp_t prop;
+    (void)hipGetDevice(&dev);
+    (void)hipGetDeviceProperties(&prop, dev);
+    (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kStreamWaves * 64, lds);
+    const int blocks = (per_cu > 0 ? (per_cu < 2 ? per_cu : 2) : 1) * prop.multiProcessorCount;
+    if (used < 64) cache[used++] = {kernel, lds, blocks};
+    return blocks;
 }
 
 template <class K> hipError_t launch_stream(K kernel, const MvArgs& a, size_t lds, hipStream_t stream) {
     int blocks = (a.groups + kStreamWaves - 1) / kStreamWaves;
-    const int cap = resident_blocks(kernel, lds);
+    const int cap = resident_blocks(reinterpret_cast<const void*>(kernel), lds);
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
     launch_kernel(kernel, dim3(blocks), dim3(kStreamWaves * 64), lds, stream, a);
@@ -773,6 +794,7 @@ hipError_t launch_matvec_stream(uint32_t type, bool q8, const MvArgs& a, hipStre
                    ((a.head_dim / 4) & (a.head_dim / 4 - 1)) || a.cols % a.head_dim))
         return hipErrorInvalidValue;
     if (a.rows_per_group != (a.mode == kMvSwiglu ? kMvStreamPairRows : kMvStreamRows)) return hipErrorInvalidValue;
+    if (a.silu_mask && !a.conv_w) return hipErrorInvalidValue;  // SiLU'd segments ride with the conv epilogue
     // the conv epilogue holds an item's rows x taps in the lanes of one wave
     if (a.conv_w && (a.mode == kMvSwiglu || a.conv_width < 1 || a.conv_width * a.rows_per_group > 64))
         return hipErrorInvalidValue;

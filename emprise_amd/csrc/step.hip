@@ -395,7 +395,11 @@ __device__ void step_matvec(const StepMatvec& m, uint32_t tag, uint32_t base, un
                             st_out(m.seg[s].y, row, siluf_(acc[r]) * acc[(R + r) % NA], tag);
                         } else {
                             float v = acc[r];
-                            if ((m.silu_mask >> s) & 1) v = siluf_(v);  // wave-uniform
+                            if constexpr (CONV)  // (see the streaming kernel)
+                                if ((m.silu_mask >> s) & 1) {
+                                    asm volatile("" : "+v"(v));
+                                    v = siluf_(v);
+                                }
                             if (m.seg[s].y.p) st_out(m.seg[s].y, row, v, tag);
                             if (m.mode == kMvArgmax) {
                                 const unsigned long long k = argmax_key(acc[r], row);
