@@ -1,7 +1,12 @@
 // Gated DeltaNet decode step on gfx950 (Backend::delta_net, reference
 // backend.cpp:19-60; the CUDA delta_conv/delta_scan/delta_norm_gate, cuda.cpp:417-479).
 //
-// One workgroup per value head (8 waves). The head's q/k are L2-normalised inside the
+// Two forms. gdn_rows_kernel (the recurrent block's path when the out-projection is in
+// the chunked layout) splits each head's rows over SPLIT workgroups and writes the raw
+// outputs S.q; the per-head RMSNorm x gate then runs in the out-projection's input
+// staging, and the gate rows arrive already SiLU'd from the in-projection. gdn_kernel
+// (Backend::delta_net, and the other out-projection widths) does the whole head:
+// one workgroup per value head (8 waves). The head's q/k are L2-normalised inside the
 // workgroup (every wave redundantly; 2*state_dim values), the 64 KiB state of the head
 // is streamed once -- each wave loads all of its rows before any arithmetic so the
 // reads overlap -- updated in registers and written back, and the per-head RMSNorm x

@@ -4,7 +4,11 @@
 // (Backend::linear / linear_many / the gate+up half of feed_forward,
 // reference cuda.cpp:199-304, 499-532, 567-596).
 //
-// Mapping: a workgroup of 4 waves stages the input vector once in LDS (with the
+// Two kernels share this structure. Rows whose width is a multiple of 4096 (every
+// projection of the qwen35 shapes) run in matvec_stream_kernel: workgroups of 8 waves,
+// items of one row x one 4096-column chunk, two items in flight per wave (see the
+// streaming section below). Other widths run in matvec_kernel over the unit-major
+// layout: a workgroup of 4 waves stages the input vector once in LDS (with the
 // residual add + RMSNorm of the reference's dev_add/dev_rmsnorm fused in, and the
 // per-unit input sums the zero-point terms need), then each wave takes groups of R
 // rows. In a group, lane l handles units l, l+64, l+128, ... of every row, so one
@@ -232,7 +236,8 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
 
 // ---- streaming kernel for rows in the chunked layout (cols % 4096 == 0) --------------
 //
-// A wave walks a sequence of items (a group of R rows x one 4096-column chunk) and
+// A wave walks a sequence of items (R rows, or R gate/up row pairs, x one 4096-column
+// chunk; R = kMvStreamRows / kMvStreamPairRows) and
 // keeps the next item's weights in flight while it computes the current one; the
 // first item's loads go out before the workgroup stages its input. Lane l owns 64
 // consecutive weights of every chunk row: per row and chunk it issues three (Q6_K) or
