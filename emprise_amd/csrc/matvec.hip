@@ -5,8 +5,8 @@
 // reference cuda.cpp:199-304, 499-532, 567-596).
 //
 // Two kernels share this structure. Rows whose width is a multiple of 4096 (every
-// projection of the qwen35 shapes) run in matvec_stream_kernel: workgroups of 8 waves,
-// items of one row x one 4096-column chunk, two items in flight per wave (see the
+// projection of the qwen35 shapes) run in matvec_stream_kernel: workgroups of 8 or 16
+// waves, items of one row x one 4096-column chunk, one item in flight per wave (see the
 // streaming section below). Other widths run in matvec_kernel over the unit-major
 // layout: a workgroup of 4 waves stages the input vector once in LDS (with the
 // residual add + RMSNorm of the reference's dev_add/dev_rmsnorm fused in, and the
@@ -237,9 +237,12 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
 // ---- streaming kernel for rows in the chunked layout (cols % 4096 == 0) --------------
 //
 // A wave walks a sequence of items (R rows, or R gate/up row pairs, x one 4096-column
-// chunk; R = kMvStreamRows / kMvStreamPairRows) and
-// keeps the next item's weights in flight while it computes the current one; the
-// first item's loads go out before the workgroup stages its input. Lane l owns 64
+// chunk; R = kMvStreamRows / kMvStreamPairRows), with kStreamDepth items in flight: it
+// issues the loads of the item kStreamDepth ahead as soon as it has computed one, and
+// the first items' loads go out before the workgroup stages its input. One item in
+// flight measured fastest in the 9B-shape decode (543.0 tok/s, against 510.0 with two
+// and 464.1 with three): the other waves of the CU hide a wave's load latency, and the
+// fewer requests in flight the better the memory system streams them. Lane l owns 64
 // consecutive weights of every chunk row: per row and chunk it issues three (Q6_K) or
 // two (Q4_K) 16-byte loads that each cover 1 KiB contiguous across the wave, plus one
 // scale load and one d load. Row pointers are wave-uniform (scalar registers).
@@ -483,7 +486,7 @@ __device__ __forceinline__ void sinput_issue(const MvArgs& a, SInput<SB, DN>& s)
 // x_out), RMSNorm, the LDS store (chunk_slot order; natural order for Q8) and the
 // per-unit input sums, reduced across the UNIT/4 consecutive threads that hold a unit.
 template <int UNIT, bool Q8, int SB, bool DN>
-__device__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, float* usum, float* red) {
+__device__ __forceinline__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, float* usum, float* red) {
     const int n4 = a.cols / 4;
     const bool writer = a.x_out && blockIdx.x == 0;
     float4* xs4 = reinterpret_cast<float4*>(xs);
@@ -534,8 +537,12 @@ __device__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, flo
 #pragma unroll
     for (int k = 0; k < SB; ++k) {
         const int i = threadIdx.x + k * blockDim.x;
-        if (i < n4) xs4[Q8 ? i : chunk_slot(i)] = s.x[k];
-        if constexpr (!Q8) {
+        if constexpr (Q8) {
+            // stored by component: a whole-float4 copy under this predicate was lowered
+            // through scratch memory
+            if (i < n4) xs4[i] = make_float4(s.x[k].x, s.x[k].y, s.x[k].z, s.x[k].w);
+        } else {
+            if (i < n4) xs4[chunk_slot(i)] = s.x[k];
             float t = (s.x[k].x + s.x[k].y) + (s.x[k].z + s.x[k].w);
             t += __shfl_xor(t, 1, 64);
             t += __shfl_xor(t, 2, 64);
@@ -547,22 +554,24 @@ __device__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, flo
 
 // Staging modes of a launch: 0 generic (sstage, after the first items' loads),
 // 1 up to 4096 columns with residual add and norm, 2 up to 12288 columns, plain input.
-constexpr int kStreamWaves = 8;
-template <int SM> struct StageMode;
-template <> struct StageMode<0> { static constexpr int sb = 1; static constexpr bool dn = false; };
-template <> struct StageMode<1> { static constexpr int sb = 1024 / (kStreamWaves * 64); static constexpr bool dn = true; };
-template <> struct StageMode<2> { static constexpr int sb = 3072 / (kStreamWaves * 64); static constexpr bool dn = false; };
+// W: waves per workgroup (8 or 16; see launch_stream_mode).
+constexpr int kStreamWavesPerCU = 16;  // resident waves per CU the grid is sized for
+constexpr int kStreamDepth = 1;        // items in flight per wave
+template <int W, int SM> struct StageMode;
+template <int W> struct StageMode<W, 0> { static constexpr int sb = 1; static constexpr bool dn = false; };
+template <int W> struct StageMode<W, 1> { static constexpr int sb = 1024 / (W * 64); static constexpr bool dn = true; };
+template <int W> struct StageMode<W, 2> { static constexpr int sb = 3072 / (W * 64); static constexpr bool dn = false; };
 
-template <int T, bool Q8, bool PAIR, bool CONV, int SM>
-__global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs a) {
+template <int T, bool Q8, bool PAIR, bool CONV, int SM, int W>
+__global__ __launch_bounds__(W * 64) void matvec_stream_kernel(MvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ float red[kStreamWaves];
+    __shared__ float red[W];
     __shared__ unsigned long long block_best;
     constexpr int R = PAIR ? kMvStreamPairRows : kMvStreamRows;
     constexpr int UW = Fmt<T>::unit;
     constexpr int NA = PAIR ? R * 2 : R;
-    constexpr int SB = StageMode<SM>::sb;
-    constexpr bool DN = StageMode<SM>::dn;
+    constexpr int SB = StageMode<W, SM>::sb;
+    constexpr bool DN = StageMode<W, SM>::dn;
     float* xs = reinterpret_cast<float*>(smem);
     float* usum = xs + a.cols;
     const int units = a.cols / UW;
@@ -574,7 +583,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int cpr = a.cols / kChunkCols;
     const size_t row_bytes = (size_t)(a.cols / 256) * Fmt<T>::block;
-    const int stride = gridDim.x * kStreamWaves;
+    const int stride = gridDim.x * W;
     const uint8_t* dummy = reinterpret_cast<const uint8_t*>(a.x);
 
     // row pointers of item `it`'s row group
@@ -591,7 +600,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
             it.rp[r] = (r < R ? a.seg[s].w : a.seg[1].w) + (size_t)rc * row_bytes;
         }
     };
-    // moves `it` n items ahead in this wave's sequence (n <= 2 * chunks per row)
+    // moves `it` n items ahead in this wave's sequence
     auto skip = [&](SItem<NA>& it, int n) {
         const int c = it.c + n, hop = c / cpr;
         it.c = c - hop * cpr;
@@ -620,24 +629,29 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
         }
     };
 
-    // Input loads first, then the weights of the wave's first two items, then the
+    // Input loads first, then the weights of the wave's first D items, then the
     // staging arithmetic: the loads return in issue order, so the staging waits only
     // for its own (L2-resident) data while the weight streams are in flight.
-    // (sched_barrier keeps the three groups of loads in this order: the wait for
-    // buffer A must not cover any of B's loads.)
+    // (sched_barrier keeps the groups of loads in this order: the wait for one buffer
+    // must not cover the loads of the next.)
     SInput<SB, DN> sin;
     if constexpr (SM != 0) sinput_issue<SB, DN>(a, sin);
-    SItem<NA> ia, ib;
-    ia.g = blockIdx.x * kStreamWaves + wave;
-    ia.c = 0;
-    if (ia.g < a.groups) rows_of(ia);
-    ib = ia;
-    skip(ib, 1);
-    SChunk<T, NA> A, B;
-    __builtin_amdgcn_sched_barrier(0);
-    iload(A, ia);
-    __builtin_amdgcn_sched_barrier(0);
-    iload(B, ib);
+    constexpr int D = kStreamDepth;
+    SItem<NA> its[D];
+    its[0].g = blockIdx.x * W + wave;
+    its[0].c = 0;
+    if (its[0].g < a.groups) rows_of(its[0]);
+#pragma unroll
+    for (int k = 1; k < D; ++k) {
+        its[k] = its[k - 1];
+        skip(its[k], 1);
+    }
+    SChunk<T, NA> bufs[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        __builtin_amdgcn_sched_barrier(0);
+        iload(bufs[k], its[k]);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (SM != 0) sinput_finish<UW, Q8, SB, DN>(a, sin, xs, usum, red);
@@ -655,7 +669,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
     for (int r = 0; r < NA; ++r) acc[r] = 0.f;
 
     // Computes the item held in `buf`, runs the row epilogue after a row group's last
-    // chunk, then refills `buf` with the item two ahead (the other buffer holds the next).
+    // chunk, then refills `buf` with the item D ahead (the other buffers hold the next).
     auto process = [&](SChunk<T, NA>& buf, SItem<NA>& it) {
         if constexpr (Q8) scompute_q8<NA>(buf, acc, xq, xscale, qsum, it.c, lane);
         else scompute<T, NA>(buf, acc, xs, usum, it.c, lane);
@@ -709,13 +723,19 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
 #pragma unroll
             for (int r = 0; r < NA; ++r) acc[r] = 0.f;
         }
-        skip(it, 2);
+        skip(it, D);
         iload(buf, it);
     };
-    while (ia.g < a.groups) {
-        process(A, ia);
-        if (ib.g >= a.groups) break;
-        process(B, ib);
+    // items are visited in sequence order, so once one is past the end so are the rest
+    bool live = its[0].g < a.groups;
+    while (live) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            if (live) {
+                process(bufs[k], its[k]);
+                live = its[(k + 1) % D].g < a.groups;
+            }
+        }
     }
     if (a.mode == kMvArgmax) {
         if (lane == 0 && best) atomicMax(&block_best, best);
@@ -725,12 +745,13 @@ __global__ __launch_bounds__(kStreamWaves * 64) void matvec_stream_kernel(MvArgs
 }
 
 // Workgroups of a streaming launch: one full round of resident workgroups (occupancy x
-// CUs, at most two per CU), so no wave waits for a second dispatch round. Occupancy
-// differs per kernel instantiation (registers) and per LDS size, so the cache is keyed
-// by both. The cap: every workgroup stages the whole input, and a third workgroup per CU
-// (the one-row kernels have room for it) measured slower in the 9B-shape decode (508.4
-// vs 513.5 tok/s; one per CU 514.9, but slower on the in-projection and the LM head).
-int resident_blocks(const void* kernel, size_t lds) {
+// CUs, at most kStreamWavesPerCU waves per CU), so no wave waits for a second dispatch
+// round. Occupancy differs per kernel instantiation (registers) and per LDS size, so
+// the cache is keyed by both. The cap: every workgroup stages the whole input, and 32
+// waves per CU (four 8-wave or two 16-wave workgroups, which the one-item kernels have
+// room for) measured slower than 16 in the 9B-shape decode (526.0 and 540.7 vs 543.0
+// tok/s with 8-wave workgroups).
+int resident_blocks(const void* kernel, size_t lds, int waves) {
     struct Entry {
         const void* kernel;
         size_t lds;
@@ -746,31 +767,43 @@ int resident_blocks(const void* kernel, size_t lds) {
     hipDeviceProp_t prop;
     (void)hipGetDevice(&dev);
     (void)hipGetDeviceProperties(&prop, dev);
-    (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kStreamWaves * 64, lds);
-    const int blocks = (per_cu > 0 ? (per_cu < 2 ? per_cu : 2) : 1) * prop.multiProcessorCount;
+    (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, waves * 64, lds);
+    const int cap = kStreamWavesPerCU / waves;
+    const int blocks = (per_cu > 0 ? (per_cu < cap ? per_cu : cap) : 1) * prop.multiProcessorCount;
     if (used < 64) cache[used++] = {kernel, lds, blocks};
     return blocks;
 }
 
-template <class K> hipError_t launch_stream(K kernel, const MvArgs& a, size_t lds, hipStream_t stream) {
-    int blocks = (a.groups + kStreamWaves - 1) / kStreamWaves;
-    const int cap = resident_blocks(reinterpret_cast<const void*>(kernel), lds);
+template <int W, class K> hipError_t launch_stream(K kernel, const MvArgs& a, size_t lds, hipStream_t stream) {
+    int blocks = (a.groups + W - 1) / W;
+    const int cap = resident_blocks(reinterpret_cast<const void*>(kernel), lds, W);
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
-    launch_kernel(kernel, dim3(blocks), dim3(kStreamWaves * 64), lds, stream, a);
+    launch_kernel(kernel, dim3(blocks), dim3(W * 64), lds, stream, a);
     return hipGetLastError();
 }
 
+// Workgroup size per staging mode, both sized to 16 resident waves per CU. Measured in
+// the 9B-shape decode (one item in flight per wave): 8-wave workgroups (two per CU) are
+// faster for the launches whose staging has a residual add + RMSNorm (FFN gate+up 17.2 vs
+// 18.0 µs, GDN in-projection 12.1 vs 13.3 µs), one 16-wave workgroup per CU for the plain
+// 12288-wide input (ffn_down 9.3 vs 10.5 µs) and the per-head gated staging (GDN
+// out-projection 5.5 vs 6.8 µs). The mode sets which block reduction runs, and the two
+// 16-wave modes have none, so results do not depend on the workgroup size.
 template <int T, bool Q8, bool PAIR, bool CONV>
 hipError_t launch_stream_mode(const MvArgs& a, size_t lds, hipStream_t stream) {
-    const int threads = kStreamWaves * 64, n4 = a.cols / 4;
-    if (n4 <= StageMode<1>::sb * threads) return launch_stream(matvec_stream_kernel<T, Q8, PAIR, CONV, 1>, a, lds, stream);
+    const int n4 = a.cols / 4;
+    if (n4 <= StageMode<8, 1>::sb * 8 * 64) {
+        if constexpr (!PAIR && !CONV)
+            if (a.gate) return launch_stream<16>(matvec_stream_kernel<T, Q8, false, false, 1, 16>, a, lds, stream);
+        return launch_stream<8>(matvec_stream_kernel<T, Q8, PAIR, CONV, 1, 8>, a, lds, stream);
+    }
     if (a.gate) return hipErrorInvalidValue;  // the per-head transform stages in one pass only
     if constexpr (!CONV) {
-        if (!a.delta && !a.norm && n4 <= StageMode<2>::sb * threads)
-            return launch_stream(matvec_stream_kernel<T, Q8, PAIR, false, 2>, a, lds, stream);
+        if (!a.delta && !a.norm && n4 <= StageMode<16, 2>::sb * 16 * 64)
+            return launch_stream<16>(matvec_stream_kernel<T, Q8, PAIR, false, 2, 16>, a, lds, stream);
     }
-    return launch_stream(matvec_stream_kernel<T, Q8, PAIR, CONV, 0>, a, lds, stream);
+    return launch_stream<8>(matvec_stream_kernel<T, Q8, PAIR, CONV, 0, 8>, a, lds, stream);
 }
 
 template <int T, bool Q8> hipError_t launch_stream_kind(const MvArgs& a, size_t lds, hipStream_t stream) {
