@@ -1,7 +1,7 @@
 // Gated GQA attention decode on gfx950 (Model::Impl::attention_preout, reference
 // model.cpp:129-157, which the reference runs on the host even on its device path).
 //
-// Split-KV ("flash decoding"): workgroup (kv head, chunk of kAttnChunk positions)
+// Split-KV ("flash decoding"): workgroup (kv head, chunk of kAttnOpChunk positions)
 // serves the `group` = heads/kv_heads query heads that share the KV head, so each K/V
 // row is read once for all of them. Every workgroup recomputes the RMSNorm + RoPE of
 // its query heads and of the new key (a few KiB of work); the workgroup whose chunk
@@ -11,13 +11,13 @@
 // the sigmoid output gate. (A last-workgroup merge inside the first kernel would need
 // device-scope fences, which write back and invalidate a whole L2 on this part.)
 //
-// Inside a workgroup no output needs a cross-lane reduction chain: the chunk's keys
-// are copied to LDS and lane t of wave w computes the score of position t for query
-// head w (a 256-long dot product with the query broadcast from LDS), so the softmax
-// statistics are one wave max and one wave sum per head; for P.V, lane l of every wave
-// accumulates output dims E*l .. E*l+E-1 (head_dim = 64*E) over the wave's own value
-// rows, and the four waves' sums are added through LDS. Rows move as one 16-byte
-// (E = 4) access per lane.
+// Inside a workgroup every wave owns CH/4 positions and keeps their K and V rows in
+// registers, lane l holding dims E*l .. E*l+E-1 (head_dim = 64*E, one 16-byte access per
+// row at E = 4). A score is then E products and one wave sum, with the query heads
+// in registers too; each wave keeps its own softmax maximum and sum and accumulates
+// its rows' P.V, and the four waves are merged (max-rescaled) through LDS. Small
+// chunks keep many workgroups busy at short contexts: at 512 positions 32 chunks per
+// KV head instead of 8 with 64-position chunks.
 //
 // The grid covers the whole context so the launch can be replayed from a hipGraph:
 // the position is read from device memory and chunks past it return at once. Barriers
@@ -30,7 +30,7 @@ namespace {
 
 constexpr int kAttnWaves = 4;
 constexpr int kMaxGroup = 8;
-constexpr int kCombineMaxChunks = 1024;  // contexts up to 65536 positions
+constexpr int kCombineMaxChunks = 4096;  // contexts up to 4096 chunks
 
 // E consecutive floats (lane l of a wave owns dims E*l .. E*l+E-1 of a head): one
 // 16-, 8- or 4-byte access.
@@ -53,17 +53,11 @@ template <int E> __device__ __forceinline__ void stv(float* p, const float (&v)[
 
 template <int E>  // head_dim = 64 * E
 __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) {
-    constexpr int HD = 64 * E, CH = kAttnChunk, KS = HD + 4;  // padded key rows in LDS
-    constexpr int PW = CH / kAttnWaves;                       // rows per wave
+    constexpr int HD = 64 * E, CH = kAttnOpChunk, PW = CH / kAttnWaves;  // rows per wave
     __shared__ __align__(16) float qs[kMaxGroup][HD];
     __shared__ __align__(16) float knew[HD], vnew[HD];
-    __shared__ float sc[kMaxGroup][CH];
-    __shared__ float mstat[kMaxGroup], lstat[kMaxGroup];
-    // the chunk's keys during the scores, then the waves' P.V sums
-    constexpr int KBYTES = CH * KS * 4, ABYTES = kAttnWaves * kMaxGroup * HD * 4;
-    __shared__ __align__(16) unsigned char kv_lds[KBYTES > ABYTES ? KBYTES : ABYTES];
-    float (*ks)[KS] = reinterpret_cast<float (*)[KS]>(kv_lds);
-    float (*acc_lds)[kMaxGroup][HD] = reinterpret_cast<float (*)[kMaxGroup][HD]>(kv_lds);
+    __shared__ float wstat[kAttnWaves][kMaxGroup][2];  // per wave and head: max, sum
+    __shared__ __align__(16) float acc_lds[kAttnWaves][kMaxGroup][HD];
 
     const int group = a.heads / a.kv_heads;
     const int chunks_max = (a.context + CH - 1) / CH;
@@ -82,8 +76,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     // normalises heads w, w+4, ... and, as head `group`, the new key), then all of the
     // wave's K and V rows. The norm inputs are loaded unconditionally (clamped heads) so
     // waiting for them never waits for the K/V rows, whose latency overlaps the norms
-    // and RoPE. (Wave w owns positions t0 + w, t0 + w + 4, ...; the row at `pos` is not
-    // written yet and is replaced by the new k/v.)
+    // and RoPE. (Wave w owns positions t0 + w, t0 + w + 4, ...; rows past the chunk's
+    // end are loaded clamped and never used; the row at `pos` is not written yet, may
+    // hold anything, NaN included, and is replaced by the new k/v.)
     constexpr int NJ = (kMaxGroup + kAttnWaves) / kAttnWaves;  // heads per wave, incl. the key
     float xin[NJ][E], qn[E], kn[E];
 #pragma unroll
@@ -104,11 +99,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     float kr[PW][E], vr[PW][E];
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-        const int tt = wave + kAttnWaves * i;
-        if (tt < tn) {
-            ldv<E>(kr[i], kb + (size_t)tt * row_stride);
-            ldv<E>(vr[i], vb + (size_t)tt * row_stride);
-        }
+        const int tt = min(wave + kAttnWaves * i, tn - 1);
+        ldv<E>(kr[i], kb + (size_t)tt * row_stride);
+        ldv<E>(vr[i], vb + (size_t)tt * row_stride);
     }
 
     // RMSNorm of the query heads and of the new key (model.cpp:133-134)
@@ -147,84 +140,98 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
             a.values[((size_t)pos * a.kv_heads + kvh) * HD + d] = vnew[d];
         }
     }
-    // the chunk's keys to LDS, row-major (the new key from LDS)
-#pragma unroll
-    for (int i = 0; i < PW; ++i) {
-        const int tt = wave + kAttnWaves * i;
-        if (tt < tn) {
-            if (t0 + tt == pos) ldv<E>(kr[i], knew + E * lane);
-            stv<E>(ks[tt] + E * lane, kr[i]);
-        }
-    }
-    lds_barrier();
 
-    // scores and chunk-local softmax: wave w takes query heads w, w+4, ...; lane t is
-    // position t0 + t (model.cpp:143-150)
-    const float inv_root = 1.f / sqrtf((float)HD);
-    for (int g = wave; g < group; g += kAttnWaves) {
-        float s = -INFINITY;
-        if (lane < tn) {
-            const float4* k4 = reinterpret_cast<const float4*>(ks[lane]);
-            const float4* q4 = reinterpret_cast<const float4*>(qs[g]);
-            float dx = 0.f, dy = 0.f, dz = 0.f, dw = 0.f;  // four chains, not one long one
-#pragma unroll 16
-            for (int i = 0; i < HD / 4; ++i) {
-                const float4 k = k4[i], q = q4[i];
-                dx = fmaf(q.x, k.x, dx);
-                dy = fmaf(q.y, k.y, dy);
-                dz = fmaf(q.z, k.z, dz);
-                dw = fmaf(q.w, k.w, dw);
-            }
-            s = ((dx + dy) + (dz + dw)) * inv_root;
-        }
-        const float m = wave_max(s);
-        const float p = lane < tn ? expf(s - m) : 0.f;
-        const float l = wave_sum(p);
-        sc[g][lane] = p;
-        if (lane == 0) {
-            mstat[g] = m;
-            lstat[g] = l;
-        }
-    }
-    lds_barrier();  // scores done: the key tile's LDS now takes the P.V sums
-
-    // o[g] = sum_t p[g][t] v_t over this wave's positions
-    float acc[kMaxGroup][E];
+    // Scores of the wave's rows (model.cpp:143-150): lane l holds dims E*l .. E*l+E-1
+    // of every query head and of the row, so a score is E products and one wave sum.
+    // The softmax statistics are kept per wave (its own maximum) and merged below.
+    float qv[kMaxGroup][E];
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g)
+        if (g < group) ldv<E>(qv[g], qs[g] + E * lane);
+    const float inv_root = 1.f / sqrtf((float)HD);
+    float sc[PW][kMaxGroup];
+    float mw[kMaxGroup];
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
+    for (int g = 0; g < kMaxGroup; ++g) mw[g] = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
         const int tt = wave + kAttnWaves * i;
-        if (tt < tn) {
-            if (t0 + tt == pos) ldv<E>(vr[i], vnew + E * lane);
+        if (t0 + tt == pos) {
+            ldv<E>(kr[i], knew + E * lane);
+            ldv<E>(vr[i], vnew + E * lane);
+        }
 #pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
-                if (g < group) {
-                    const float p = sc[g][tt];
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g < group) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < E; ++e) d = fmaf(qv[g][e], kr[i][e], d);
+                const float s = wave_sum(d) * inv_root;
+                sc[i][g] = tt < tn ? s : -INFINITY;
+                mw[g] = fmaxf(mw[g], sc[i][g]);
+            }
+        }
+    }
+    // o_w[g] = sum_t exp(s - m_w) v_t over the wave's rows
+    float acc[kMaxGroup][E];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        float lw = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
+        if (g < group) {
+#pragma unroll
+            for (int i = 0; i < PW; ++i) {
+                // (rows past the chunk's end hold a clamped copy of the row at `pos`,
+                // which the cache does not have yet: never touched, not even times 0)
+                if (wave + kAttnWaves * i < tn) {
+                    const float p = expf(sc[i][g] - mw[g]);
+                    lw += p;
 #pragma unroll
                     for (int e = 0; e < E; ++e) acc[g][e] = fmaf(p, vr[i][e], acc[g][e]);
                 }
             }
+            stv<E>(acc_lds[wave][g] + E * lane, acc[g]);
+            if (lane == 0) {
+                wstat[wave][g][0] = mw[g];
+                wstat[wave][g][1] = lw;
+            }
         }
     }
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
-        if (g < group) stv<E>(acc_lds[wave][g] + E * lane, acc[g]);
     lds_barrier();
+    // Merge of the waves (max-rescaled sums) into the chunk's partial: o, max, sum.
+    // Lane w*8+g of every wave computes the weight exp(m_w - M_g) of wave w for head g.
+    float wgt = 0.f, mg = -INFINITY;
+    if (lane < kAttnWaves * kMaxGroup) {
+        const int w = lane >> 3, g = lane & 7;
+        if (g < group) {
+#pragma unroll
+            for (int v = 0; v < kAttnWaves; ++v) mg = fmaxf(mg, wstat[v][g][0]);
+            const float m = wstat[w][g][0];
+            wgt = m == -INFINITY ? 0.f : expf(m - mg);
+        }
+    }
     const int stride = HD + 2;
     float* part = a.partial + ((size_t)kvh * chunks_max + chunk) * group * stride;
     for (int idx = threadIdx.x; idx < group * HD; idx += blockDim.x) {
         const int g = idx / HD, d = idx % HD;
         float o = 0.f;
 #pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) o += acc_lds[w][g][d];
+        for (int w = 0; w < kAttnWaves; ++w) o = fmaf(__shfl(wgt, w * 8 + g, 64), acc_lds[w][g][d], o);
         part[g * stride + d] = o;
     }
-    if (threadIdx.x < group) {
-        part[threadIdx.x * stride + HD] = mstat[threadIdx.x];
-        part[threadIdx.x * stride + HD + 1] = lstat[threadIdx.x];
+    if (wave == 0) {
+        float l = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const int g = lane < kMaxGroup ? lane : 0;
+            l = fmaf(__shfl(wgt, w * 8 + g, 64), wstat[w][g][1], l);
+        }
+        const float m = __shfl(mg, lane < kMaxGroup ? lane : 0, 64);
+        if (lane < group) {
+            part[lane * stride + HD] = m;
+            part[lane * stride + HD + 1] = l;
+        }
     }
 }
 
@@ -243,8 +250,8 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
     const int pos = *a.position;
     if (pos < 0 || pos >= a.context) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunks_max = (a.context + kAttnChunk - 1) / kAttnChunk;
-    const int nchunks = pos / kAttnChunk + 1;
+    const int chunks_max = (a.context + kAttnOpChunk - 1) / kAttnOpChunk;
+    const int nchunks = pos / kAttnOpChunk + 1;
     const int kvh = head / group, g = head - kvh * group, stride = hd + 2;
     const float* base = a.partial + ((size_t)kvh * chunks_max * group + g) * stride;
     const size_t cstride = (size_t)group * stride;
@@ -302,14 +309,15 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
 }  // namespace
 
 size_t attention_partial_floats(int heads, int kv_heads, int head_dim, int context) {
-    const int chunks = (context + kAttnChunk - 1) / kAttnChunk;
+    // sized for the per-op kernel's chunks, which are no longer than the step program's
+    const int chunks = (context + kAttnOpChunk - 1) / kAttnOpChunk;
     return (size_t)kv_heads * chunks * (heads / kv_heads) * (head_dim + 2);
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
     if (a.heads % a.kv_heads || a.heads / a.kv_heads > kMaxGroup || a.rotary > a.head_dim || a.rotary % 2)
         return hipErrorInvalidValue;
-    const int chunks = (a.context + kAttnChunk - 1) / kAttnChunk;
+    const int chunks = (a.context + kAttnOpChunk - 1) / kAttnOpChunk;
     if (chunks > kCombineMaxChunks) return hipErrorInvalidValue;
     const dim3 grid(a.kv_heads * chunks), block(kAttnWaves * 64);
     switch (a.head_dim) {

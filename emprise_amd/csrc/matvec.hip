@@ -242,7 +242,9 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
 // the first items' loads go out before the workgroup stages its input. One item in
 // flight measured fastest in the 9B-shape decode (543.0 tok/s, against 510.0 with two
 // and 464.1 with three): the other waves of the CU hide a wave's load latency, and the
-// fewer requests in flight the better the memory system streams them. Lane l owns 64
+// fewer requests in flight the better the memory system streams them. Issuing the next
+// item as soon as the current one has arrived (two buffers, still one item in flight,
+// the loads overlapping the arithmetic) measured 2% slower than issuing it after. Lane l owns 64
 // consecutive weights of every chunk row: per row and chunk it issues three (Q6_K) or
 // two (Q4_K) 16-byte loads that each cover 1 KiB contiguous across the wave, plus one
 // scale load and one d load. Row pointers are wave-uniform (scalar registers).
@@ -670,7 +672,7 @@ __global__ __launch_bounds__(W * 64) void matvec_stream_kernel(MvArgs a) {
 
     // Computes the item held in `buf`, runs the row epilogue after a row group's last
     // chunk, then refills `buf` with the item D ahead (the other buffers hold the next).
-    auto process = [&](SChunk<T, NA>& buf, SItem<NA>& it) {
+    auto finish = [&](SChunk<T, NA>& buf, SItem<NA>& it) {
         if constexpr (Q8) scompute_q8<NA>(buf, acc, xq, xscale, qsum, it.c, lane);
         else scompute<T, NA>(buf, acc, xs, usum, it.c, lane);
         if (it.c == cpr - 1) {
@@ -723,8 +725,6 @@ __global__ __launch_bounds__(W * 64) void matvec_stream_kernel(MvArgs a) {
 #pragma unroll
             for (int r = 0; r < NA; ++r) acc[r] = 0.f;
         }
-        skip(it, D);
-        iload(buf, it);
     };
     // items are visited in sequence order, so once one is past the end so are the rest
     bool live = its[0].g < a.groups;
@@ -732,7 +732,9 @@ __global__ __launch_bounds__(W * 64) void matvec_stream_kernel(MvArgs a) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             if (live) {
-                process(bufs[k], its[k]);
+                finish(bufs[k], its[k]);
+                skip(its[k], D);
+                iload(bufs[k], its[k]);
                 live = its[(k + 1) % D].g < a.groups;
             }
         }
