@@ -122,7 +122,8 @@ struct AttnArgs {
     float* partial;  // scratch: [kv_heads][chunks][group][head_dim + 2]
 };
 constexpr int kAttnChunk = 64;    // positions per partial of the step program's attention
-constexpr int kAttnOpChunk = 16;  // positions per workgroup of attention_kernel
+constexpr int kAttnSub = 16;     // positions per step of attention_kernel's online softmax
+constexpr int kAttnSplit = 64;   // position ranges (workgroups) per KV head of attention_kernel
 size_t attention_partial_floats(int heads, int kv_heads, int head_dim, int context);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 
