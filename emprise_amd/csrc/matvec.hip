@@ -602,12 +602,31 @@ __global__ __launch_bounds__(W * 64) void matvec_stream_kernel(MvArgs a) {
             it.rp[r] = (r < R ? a.seg[s].w : a.seg[1].w) + (size_t)rc * row_bytes;
         }
     };
+    // Item order. Round-robin (wave v takes groups v, v + nw, v + 2nw, ... with nw waves
+    // in the grid), except for the SwiGLU pair launches with two workgroups per CU: the
+    // second workgroup on a CU finishes its input staging ~3 us after the first (its
+    // input loads queue behind the first one's weight loads), and its waves end that much
+    // later. There the second round goes to the first workgroups only (nw/2 groups) and
+    // the full rounds follow, so a first-workgroup wave takes one group more (two more when
+    // the last, partial round reaches only them: 4 against 2 in the 9B FFN gate+up, which
+    // then takes 16.6 instead of 17.1 us).
+    const bool tilt = PAIR && W == 8 && kStreamDepth == 1 && gridDim.x % 2 == 0;
+    const int vw = blockIdx.x * W + wave, half_nw = stride / 2;
+    const bool first_wg = (int)blockIdx.x < (int)gridDim.x / 2;
+    int later = 0;  // groups taken after the first round
     // moves `it` n items ahead in this wave's sequence
     auto skip = [&](SItem<NA>& it, int n) {
         const int c = it.c + n, hop = c / cpr;
         it.c = c - hop * cpr;
         if (hop) {
-            it.g += hop * stride;
+            if (tilt && hop == 1) {
+                // rounds after the first: [stride, stride + nw/2) for the first workgroups,
+                // then full rounds of nw groups from stride + nw/2
+                const int k = ++later, full = first_wg ? k - 2 : k - 1;
+                it.g = full < 0 ? stride + vw : stride + half_nw + full * stride + vw;
+            } else {
+                it.g += hop * stride;
+            }
             if (it.g < a.groups) rows_of(it);
         }
     };
