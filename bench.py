@@ -125,6 +125,30 @@ def traffic_from_profiles(model: str, kernel: str):
     return None if rec is None else rec.get("bytes_per_launch")
 
 
+def attention_probe(kv_len: int, calls: int = 40):
+    """Eager decode attention at the 9B shape (16 Q / 4 KV heads x 256, RoPE 64) over a
+    KV cache of kv_len positions, `calls` launches from the host, for profilers (counters
+    per dispatch): one attention + merge per call, seeded synthetic caches and inputs."""
+    import numpy as np
+    import emprise_amd as ea
+    be = ea.HipBackend(0)
+    rng = np.random.default_rng(2)
+    heads, kv, hd, rot, context = 16, 4, 256, 64, 4096
+    kvd = kv * hd
+    keys = be.to_device(rng.standard_normal((context, kvd)).astype(np.float32))
+    values = be.to_device(rng.standard_normal((context, kvd)).astype(np.float32))
+    qkv = be.to_device(rng.standard_normal(heads * hd * 2 + 2 * kvd).astype(np.float32))
+    qn, kn = be.vector(np.ones(hd, np.float32)), be.vector(np.ones(hd, np.float32))
+    ao = be.alloc(heads * hd * 4)
+    pos = be.to_device(np.array([kv_len - 1], np.int32))
+    pa = ea.AttentionParams(heads, kv, hd, rot, context, 1e-6, 1e7, qn, kn, keys, values, pos)
+    for _ in range(calls):
+        be.attention(pa, qkv, ao)
+    be.sync()
+    be.close()
+    log(f"{calls} attention calls at {kv_len} positions")
+
+
 def _graph_time_ms(be, fn, n=20, reps=5):
     """Mean duration of `fn`'s launches, replayed n times per graph, reps graphs."""
     fn()
@@ -253,6 +277,8 @@ def main():
                     help="replay each step as the persistent step kernel instead of the per-op graph")
     ap.add_argument("--copy-probe", type=int, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--attention-probe", type=int, metavar="KV_LEN",
+                    help="only run 40 eager 9B-shape attention calls over KV_LEN positions (for profilers) and exit")
     ap.add_argument("--suite", action="store_true",
                     help="only run the other benchmark configurations (C1, C2, C4), one JSON line each")
     args = ap.parse_args()
@@ -262,6 +288,9 @@ def main():
         sys.exit(2)
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.attention_probe:
+        attention_probe(args.attention_probe)
         return
     if args.suite:
         suite(args)
@@ -292,21 +321,27 @@ def main():
     program = model.step_program == 1
     log(f"prefill {args.prompt} tokens in {arrivals[0]:.3f}s, {args.steps} decode steps in {decode_s:.4f}s "
         f"-> {value:.1f} tok/s (host wall {wall:.3f}s; "
-        f"{'persistent step kernel' if program else 'per-op step graph'})")
+        f"{'persistent step kernel' if program else 'per-op launches, no graph' if args.no_graph else 'per-op step graph'})")
 
     # per-kernel timing of eager steps right after the timed region (same positions range)
     trace = []
     tok = tokens[-1]
     for _ in range(args.trace_steps):
         trace += model.trace_step(tok)
-    name, launches, bpl, mspl, share, agg = dominant_kernel(trace)
-    achieved = bpl / (mspl * 1e-3) / 1e9
-    per_kernel = {k: {"launches": v[0] // args.trace_steps, "ms_per_step": round(v[2] / args.trace_steps, 4),
-                      "GBps": round(v[1] / (v[2] * 1e-3) / 1e9, 1) if v[2] > 0 else None}
-                  for k, v in sorted(agg.items(), key=lambda kv: -kv[1][2])}
-    log(f"dominant kernel {name}: {launches // args.trace_steps} launches/step, {bpl / 1e6:.2f} MB and "
-        f"{mspl * 1e3:.2f} us per launch -> {achieved:.0f} GB/s ({share * 100:.0f}% of traced step time)")
-    log("per kernel: " + json.dumps(per_kernel))
+    roofline, per_kernel = None, None
+    if trace:
+        name, launches, bpl, mspl, share, agg = dominant_kernel(trace)
+        achieved = bpl / (mspl * 1e-3) / 1e9
+        per_kernel = {k: {"launches": v[0] // args.trace_steps, "ms_per_step": round(v[2] / args.trace_steps, 4),
+                          "GBps": round(v[1] / (v[2] * 1e-3) / 1e9, 1) if v[2] > 0 else None}
+                      for k, v in sorted(agg.items(), key=lambda kv: -kv[1][2])}
+        log(f"dominant kernel {name}: {launches // args.trace_steps} launches/step, {bpl / 1e6:.2f} MB and "
+            f"{mspl * 1e3:.2f} us per launch -> {achieved:.0f} GB/s ({share * 100:.0f}% of traced step time)")
+        log("per kernel: " + json.dumps(per_kernel))
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(args.model, name),
+                    "kernel": name, "bytes_per_launch": int(bpl), "us_per_launch": round(mspl * 1e3, 3),
+                    "launches_per_step": launches // args.trace_steps}
     model.close()
 
     e2e_gbs = value * info.token_weight_bytes / 1e9
@@ -338,10 +373,7 @@ def main():
                    "step": "persistent step kernel" if program else "per-op graph",
                    "parallelism": "single GPU"},
         "hbm_roofline_fraction": round(e2e_gbs / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(args.model, name), "kernel": name,
-                     "bytes_per_launch": int(bpl), "us_per_launch": round(mspl * 1e3, 3),
-                     "launches_per_step": launches // args.trace_steps},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": per_kernel,
     }

@@ -96,6 +96,7 @@ def hip_lib() -> ctypes.CDLL:
         "emprise_hip_argmax": (st, [vp, u64, i32, u64]),
         "emprise_hip_quantize_q8": (st, [vp, u64, i32, u64, u64]),
         "emprise_hip_delta_net": (st, [vp, vp]),
+        "emprise_hip_delta_net_batch": (st, [vp, vp, i32, u64, u64]),
         "emprise_hip_recurrent": (st, [vp, vp, vp, u64, u64]),
         "emprise_hip_attention": (st, [vp, vp, u64, u64]),
         "emprise_hip_reset_state": (st, [vp]),
@@ -296,6 +297,11 @@ class HipBackend:
 
     def delta_net(self, p: DeltaNetParams):
         self._check(self.lib.emprise_hip_delta_net(self.h, ctypes.byref(p)))
+
+    def delta_net_batch(self, p: DeltaNetParams, count: int, stride: int, out_stride: int):
+        """delta_net over `count` positions: row t of qkv/gate/alpha/beta at t*stride floats,
+        row t of out at t*out_stride floats."""
+        self._check(self.lib.emprise_hip_delta_net_batch(self.h, ctypes.byref(p), count, stride, out_stride))
 
     def recurrent(self, p: RecurrentParams, x: int, y: int, inp: Input | None = None):
         self._check(self.lib.emprise_hip_recurrent(self.h, ctypes.byref(p), ctypes.byref(inp) if inp else None, x, y))

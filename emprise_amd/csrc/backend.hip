@@ -940,6 +940,53 @@ emprise_status emprise_hip_delta_net(emprise_hip* h, const emprise_hip_delta_net
     return traced(h, "gdn_step", gdn_bytes(g), [&] { return launch_gdn(g, h->stream); });
 }
 
+emprise_status emprise_hip_delta_net_batch(emprise_hip* h, const emprise_hip_delta_net_params* p, int count,
+                                           uint64_t stride, uint64_t out_stride) {
+    if (!h || !p) return fail(EMPRISE_EINVAL, "null argument");
+    const int kd = p->key_heads * p->state_dim, vd = p->value_heads * p->state_dim, ch = 2 * kd + vd;
+    const Weight *conv = h->weight(p->conv), *a = h->weight(p->ssm_a), *dt = h->weight(p->dt), *nw = h->weight(p->norm);
+    if (p->key_heads < 1 || p->value_heads % p->key_heads || (p->state_dim != 64 && p->state_dim != 128) ||
+        p->conv_width < 1 || p->conv_width > 8 || !conv || !a || !dt || !nw ||
+        conv->rows * conv->cols != (uint64_t)ch * p->conv_width || a->rows * a->cols != (uint64_t)p->value_heads ||
+        dt->rows * dt->cols != (uint64_t)p->value_heads || nw->rows * nw->cols != (uint64_t)p->state_dim ||
+        conv->type != kF32 || a->type != kF32 || dt->type != kF32 || nw->type != kF32)
+        return fail(EMPRISE_EINVAL, "Recurrent projection dimensions");
+    if (!p->qkv || !p->gate || !p->alpha || !p->beta || !p->conv_state || !p->rec_state || !p->out)
+        return fail(EMPRISE_EINVAL, "null buffer");
+    if (count < 1 || stride < (uint64_t)ch || out_stride < (uint64_t)vd)
+        return fail(EMPRISE_EINVAL, "delta_net_batch: count %d, stride %llu, out_stride %llu", count,
+                    (unsigned long long)stride, (unsigned long long)out_stride);
+    if (h->recording) return rec_unsupported(h, "batched delta_net");
+    void *conv_out, *o;
+    TRY(h->get_scratch("gdn_conv_batch", (size_t)count * ch * sizeof(float), &conv_out));
+    TRY(h->get_scratch("gdn_o_batch", (size_t)count * vd * sizeof(float), &o));
+    GdnBatchArgs g{};
+    g.key_heads = p->key_heads;
+    g.value_heads = p->value_heads;
+    g.state_dim = p->state_dim;
+    g.conv_width = p->conv_width;
+    g.count = count;
+    g.eps = p->eps;
+    g.qkv = reinterpret_cast<const float*>(p->qkv);
+    g.gate = reinterpret_cast<const float*>(p->gate);
+    g.alpha = reinterpret_cast<const float*>(p->alpha);
+    g.beta = reinterpret_cast<const float*>(p->beta);
+    g.stride = stride;
+    g.conv_w = reinterpret_cast<const float*>(conv->dev);
+    g.ssm_a = reinterpret_cast<const float*>(a->dev);
+    g.dt = reinterpret_cast<const float*>(dt->dev);
+    g.norm = reinterpret_cast<const float*>(nw->dev);
+    g.conv_state = reinterpret_cast<float*>(p->conv_state);
+    g.state = reinterpret_cast<float*>(p->rec_state);
+    g.conv_out = static_cast<float*>(conv_out);
+    g.o = static_cast<float*>(o);
+    g.out = reinterpret_cast<float*>(p->out);
+    g.out_stride = out_stride;
+    const uint64_t bytes = (uint64_t)count * (2 * (uint64_t)ch + 2 * vd + 2 * p->value_heads + 2 * vd) * 4 +
+                           2 * (uint64_t)p->value_heads * p->state_dim * p->state_dim * 4;
+    return traced(h, "gdn_batch", bytes, [&] { return launch_gdn_batch(g, h->stream); });
+}
+
 emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent_params* p, const emprise_hip_input* in,
                                      emprise_dev x, emprise_dev y) {
     if (!h || !p || !y || (!in && !x)) return fail(EMPRISE_EINVAL, "null argument");

@@ -99,6 +99,29 @@ struct GdnArgs {
     float* state;  // [value_heads][state_dim][state_dim]
     float* out;    // [value_dim]
 };
+// `count` consecutive positions of Backend::delta_net: row t of qkv/gate/alpha/beta at
+// t * stride floats from the pointers; conv_out: count * channels floats (scratch), o:
+// count * value_dim floats (scratch, the raw S.q), out: row t at t * out_stride.
+struct GdnBatchArgs {
+    int key_heads, value_heads, state_dim, conv_width, count;
+    float eps;
+    const float* qkv;
+    const float* gate;
+    const float* alpha;
+    const float* beta;
+    size_t stride;
+    const float* conv_w;
+    const float* ssm_a;
+    const float* dt;
+    const float* norm;
+    float* conv_state;
+    float* state;
+    float* conv_out;
+    float* o;
+    float* out;
+    size_t out_stride;
+};
+hipError_t launch_gdn_batch(const GdnBatchArgs& a, hipStream_t stream);
 // conv1d + SiLU over raw channels (delta_conv): out[c] = silu(conv(shifted history)).
 hipError_t launch_delta_conv(const float* qkv, const float* conv_w, float* conv_state, float* out, int channels,
                              int conv_width, hipStream_t stream);

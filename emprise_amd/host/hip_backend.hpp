@@ -74,6 +74,9 @@ public:
     }
     void dev_swiglu(emprise_dev gate, emprise_dev up, int n) { hip_check(emprise_hip_swiglu(h_, gate, up, n), "swiglu"); }
     void dev_delta_net(const emprise_hip_delta_net_params& p) { hip_check(emprise_hip_delta_net(h_, &p), "delta_net"); }
+    void dev_delta_net_batch(const emprise_hip_delta_net_params& p, int count, uint64_t stride, uint64_t out_stride) {
+        hip_check(emprise_hip_delta_net_batch(h_, &p, count, stride, out_stride), "delta_net_batch");
+    }
     void dev_argmax(emprise_dev logits, int n, emprise_dev index) { hip_check(emprise_hip_argmax(h_, logits, n, index), "argmax"); }
     void sync() { hip_check(emprise_hip_sync(h_), "sync"); }
     void graph_begin() { hip_check(emprise_hip_graph_begin(h_), "graph_begin"); }

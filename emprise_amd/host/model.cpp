@@ -393,10 +393,10 @@ std::vector<float> Model::last_hidden() {
 // Positions [0, count) of the prompt at dev_prompt_, in chunks of up to kPrefillChunk
 // tokens: every projection runs once per chunk as a GEMM on the matrix cores (the
 // reference batches 4 positions, model.cpp:355-366; here the whole chunk), the RMSNorms,
-// residual adds and SwiGLU run over all rows at once, and the position-by-position
-// parts -- the GDN conv + state update and attention, which read the state the
-// previous position left -- run per position on the decode kernels. Op order and
-// arithmetic are those of the unfused decode step.
+// residual adds and SwiGLU run over all rows at once, the GDN conv + state update runs
+// as one scan over the chunk's positions (emprise_hip_delta_net_batch), and attention,
+// which reads the K/V rows the previous positions appended, runs per position on the
+// decode kernels. Op order and arithmetic are those of the unfused decode step.
 void Model::prefill_batched(size_t count) {
     constexpr size_t kPrefillChunk = 2048;
     HipBackend& b = *backend_;
@@ -444,15 +444,12 @@ void Model::prefill_batched(size_t count) {
                 p.norm = L.ssm_norm;
                 p.conv_state = L.conv_state;
                 p.rec_state = L.rec_state;
-                for (int t = 0; t < T; ++t) {
-                    const emprise_dev row = pf_a_ + uint64_t(t) * W * 4;
-                    p.qkv = row;
-                    p.gate = row + ch * 4;
-                    p.alpha = row + (ch + vd) * 4;
-                    p.beta = row + (ch + vd + vh) * 4;
-                    p.out = pf_b_ + uint64_t(t) * vd * 4;
-                    b.dev_delta_net(p);
-                }
+                p.qkv = pf_a_;
+                p.gate = pf_a_ + ch * 4;
+                p.alpha = pf_a_ + (ch + vd) * 4;
+                p.beta = pf_a_ + (ch + vd + vh) * 4;
+                p.out = pf_b_;
+                b.dev_delta_net_batch(p, T, W, vd);
                 b.dev_linear_batch(L.out, pf_b_, vd, pf_c_, H, T);
             } else {
                 const uint64_t W = qd + 2 * kvd;

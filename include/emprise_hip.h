@@ -182,6 +182,14 @@ typedef struct {
  * (cuda.cpp:417-479): causal conv1d + SiLU, q/k L2 norm, gated delta-rule update,
  * per-head RMSNorm x SiLU(gate). qkv is not modified. */
 emprise_status emprise_hip_delta_net(emprise_hip* h, const emprise_hip_delta_net_params* p);
+/* Backend::delta_net over `count` consecutive positions, for the batched prompt prefill
+ * (the reference runs it position by position inside its 4-position prefill batches,
+ * model.cpp:355-366): qkv, gate, alpha and beta are the rows of position 0, the rows of
+ * position t are `stride` floats further; out receives `count` rows `out_stride` floats
+ * apart. Per position the same arithmetic, in the same order, as emprise_hip_delta_net,
+ * so outputs and final states equal `count` calls of it. qkv is not modified. */
+emprise_status emprise_hip_delta_net_batch(emprise_hip* h, const emprise_hip_delta_net_params* p, int count,
+                                           uint64_t stride, uint64_t out_stride);
 
 /* Backend::RecurrentBlock (backend.hpp:44-51) on device. */
 typedef struct {

@@ -153,6 +153,72 @@ def test_delta_net_steps(backend, kh, vh, sd, cw):
         assert np.array_equal(backend.download(conv_g, ch * cw), conv_c)  # conv history is a copy
 
 
+@pytest.mark.parametrize("kh,vh,sd,cw,count", [(16, 32, 128, 4, 37), (4, 8, 64, 4, 9), (4, 8, 64, 3, 1),
+                                               (16, 32, 128, 4, 1)])
+def test_delta_net_batch_matches_steps(backend, kh, vh, sd, cw, count):
+    """emprise_hip_delta_net_batch (the prefill scan over `count` positions, rows in a
+    strided [qkv | gate | alpha | beta] layout) equals `count` calls of delta_net: every
+    output row and both final states bit for bit, from a nonzero starting state; the
+    first steps are also checked against the oracle."""
+    rng = np.random.default_rng(11)
+    kd, vd = kh * sd, vh * sd
+    ch = 2 * kd + vd
+    W = ch + vd + 2 * vh + 5  # padded row stride
+    prm = _gdn_inputs(rng, kh, vh, sd, cw)
+    eps = 1e-6
+    conv0 = (rng.standard_normal(ch * cw) * 0.3).astype(np.float32)
+    rec0 = (rng.standard_normal(vh * sd * sd) * 0.05).astype(np.float32)
+    rows = rng.standard_normal((count, W)).astype(np.float32)
+    wconv, wa, wdt, wn = (backend.vector(prm[k]) for k in ("conv", "ssm_a", "dt", "norm"))
+    # position by position
+    conv_s, rec_s = backend.to_device(conv0), backend.to_device(rec0)
+    bufs = {k: backend.alloc(n * 4) for k, n in (("qkv", ch), ("gate", vd), ("alpha", vh), ("beta", vh), ("out", vd))}
+    seq = np.zeros((count, vd), np.float32)
+    conv_c, rec_c = conv0.copy(), rec0.copy()
+    for t in range(count):
+        r = rows[t]
+        parts = (("qkv", r[:ch]), ("gate", r[ch:ch + vd]), ("alpha", r[ch + vd:ch + vd + vh]),
+                 ("beta", r[ch + vd + vh:ch + vd + 2 * vh]))
+        for k, v in parts:
+            backend.upload(bufs[k], np.ascontiguousarray(v))
+        p = DeltaNetParams(kh, vh, sd, cw, eps, bufs["qkv"], bufs["gate"], bufs["alpha"], bufs["beta"], wconv, wa,
+                           wdt, wn, conv_s, rec_s, bufs["out"])
+        backend.delta_net(p)
+        seq[t] = backend.download(bufs["out"], vd)
+        if t < 2:
+            ref = oracle.delta_net(kh, vh, sd, cw, eps, r[:ch], r[ch:ch + vd], r[ch + vd:ch + vd + vh],
+                                   r[ch + vd + vh:ch + vd + 2 * vh], prm["conv"], prm["ssm_a"], prm["dt"], prm["norm"],
+                                   conv_c, rec_c)
+            _close(seq[t], ref, what=f"step {t} vs oracle")
+    # one batched call over the strided rows
+    conv_b, rec_b = backend.to_device(conv0), backend.to_device(rec0)
+    rows_d = backend.to_device(rows)
+    out_stride = vd + 3
+    out_d = backend.alloc(count * out_stride * 4)
+    p = DeltaNetParams(kh, vh, sd, cw, eps, rows_d, rows_d + ch * 4, rows_d + (ch + vd) * 4,
+                       rows_d + (ch + vd + vh) * 4, wconv, wa, wdt, wn, conv_b, rec_b, out_d)
+    backend.delta_net_batch(p, count, W, out_stride)
+    got = backend.download(out_d, count * out_stride).reshape(count, out_stride)[:, :vd]
+    assert np.array_equal(got, seq)
+    assert np.array_equal(backend.download(rec_b, vh * sd * sd), backend.download(rec_s, vh * sd * sd))
+    assert np.array_equal(backend.download(conv_b, ch * cw), backend.download(conv_s, ch * cw))
+    assert np.array_equal(backend.download(rows_d, count * W).reshape(count, W), rows)  # inputs untouched
+
+
+def test_delta_net_batch_rejects_bad_strides(backend):
+    kh, vh, sd, cw = 4, 8, 64, 4
+    kd, vd = kh * sd, vh * sd
+    ch = 2 * kd + vd
+    prm = _gdn_inputs(np.random.default_rng(0), kh, vh, sd, cw)
+    wconv, wa, wdt, wn = (backend.vector(prm[k]) for k in ("conv", "ssm_a", "dt", "norm"))
+    buf = backend.alloc(4 * (ch + vd + 2 * vh))
+    st = backend.alloc(4 * (ch * cw + vh * sd * sd))
+    p = DeltaNetParams(kh, vh, sd, cw, 1e-6, buf, buf, buf, buf, wconv, wa, wdt, wn, st, st, buf)
+    for count, stride, out_stride in ((0, ch, vd), (2, ch - 1, vd), (2, ch, vd - 1)):
+        with pytest.raises(InvalidArgument):
+            backend.delta_net_batch(p, count, stride, out_stride)
+
+
 @pytest.mark.parametrize("wtype,kh,vh,sd", [(Q6_K, 16, 32, 128), (Q4_K, 16, 32, 128), (Q6_K, 16, 64, 64)])
 def test_recurrent_block(backend, wtype, kh, vh, sd):
     """dev_recurrent: fused projections + conv epilogue + scan + out projection. With a
