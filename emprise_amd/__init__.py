@@ -99,6 +99,7 @@ def hip_lib() -> ctypes.CDLL:
         "emprise_hip_delta_net_batch": (st, [vp, vp, i32, u64, u64]),
         "emprise_hip_recurrent": (st, [vp, vp, vp, u64, u64]),
         "emprise_hip_attention": (st, [vp, vp, u64, u64]),
+        "emprise_hip_attention_batch": (st, [vp, vp, u64, i32, u64, i32, u64, u64]),
         "emprise_hip_reset_state": (st, [vp]),
         "emprise_hip_sync": (st, [vp]),
         "emprise_hip_advance": (st, [vp, u64, u64, u64, u64]),
@@ -308,6 +309,13 @@ class HipBackend:
 
     def attention(self, p: AttentionParams, qkv: int, out: int):
         self._check(self.lib.emprise_hip_attention(self.h, ctypes.byref(p), qkv, out))
+
+    def attention_batch(self, p: AttentionParams, qkv: int, count: int, stride: int, first: int, out: int,
+                        out_stride: int):
+        """attention over positions first .. first+count-1: qkv row t at t*stride floats,
+        out row t at t*out_stride floats."""
+        self._check(self.lib.emprise_hip_attention_batch(self.h, ctypes.byref(p), qkv, count, stride, first, out,
+                                                         out_stride))
 
     def advance(self, state: int, prompt: int = 0, history: int = 0, nxt: int = 0):
         self._check(self.lib.emprise_hip_advance(self.h, state, prompt, history, nxt))

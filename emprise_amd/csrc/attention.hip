@@ -357,7 +357,147 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
     }
 }
 
+// ---- batched form: `count` consecutive prompt positions (the prefill) --------------------
+//
+// Position t (absolute p0 + t) attends over 0..p0+t. The dense parts run on the matrix
+// cores through the FP32 GEMM (S = Q K^T per head, then O = P V): attn_prep_batch_kernel
+// normalises and rotates the queries and new keys exactly as attention_kernel does and
+// appends k/v to the caches; attn_softmax_batch_kernel turns a row of S into the
+// reference's exp(s - peak) / total with s = dot / sqrt(head_dim) (model.cpp:143-150)
+// and zeroes the masked keys; attn_gate_batch_kernel applies the sigmoid gate.
+
+// Workgroup = one position; wave w normalises head vectors w, w+8, ... of the group's
+// q heads (all kv heads' groups) and the kv heads' new keys.
+template <int E>
+__global__ __launch_bounds__(512) void attn_prep_batch_kernel(AttnBatchArgs a) {
+    constexpr int HD = 64 * E;
+    extern __shared__ __align__(16) float rows[];  // (heads + kv_heads) x HD
+    const int t = blockIdx.x, pos = a.first + t;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const int nh = a.heads + a.kv_heads, qd = a.heads * HD * 2, kvd = a.kv_heads * HD;
+    const float* row = a.qkv + (size_t)t * a.stride;
+    for (int v = wave; v < nh; v += waves) {
+        const bool is_q = v < a.heads;
+        const float* src = is_q ? row + (size_t)v * HD * 2 : row + qd + (size_t)(v - a.heads) * HD;
+        const float* w = is_q ? a.q_norm : a.k_norm;
+        float x[E], ss = 0.f;
+        ldv<E>(x, src + E * lane);
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss += x[e] * x[e];
+        ss = wave_sum(ss);
+        const float scale = 1.f / sqrtf(ss / (float)HD + a.eps);
+        float wv[E], y[E];
+        ldv<E>(wv, w + E * lane);
+#pragma unroll
+        for (int e = 0; e < E; ++e) y[e] = x[e] * (scale * wv[e]);
+        stv<E>(rows + (size_t)v * HD + E * lane, y);
+    }
+    __syncthreads();
+    const int half = a.rotary / 2;
+    for (int idx = threadIdx.x; idx < nh * half; idx += blockDim.x) {
+        const int v = idx / half, i = idx % half;
+        float* r = rows + (size_t)v * HD;
+        const float angle = (float)pos / powf(a.rope_base, 2.f * (float)i / (float)a.rotary);
+        const float c = cosf(angle), s = sinf(angle);
+        const float x0 = r[i], x1 = r[i + half];
+        r[i] = x0 * c - x1 * s;
+        r[i + half] = x0 * s + x1 * c;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < a.heads * HD; idx += blockDim.x) a.q[(size_t)t * a.heads * HD + idx] = rows[idx];
+    for (int idx = threadIdx.x; idx < kvd; idx += blockDim.x) {
+        a.keys[(size_t)pos * kvd + idx] = rows[(size_t)a.heads * HD + idx];
+        a.values[(size_t)pos * kvd + idx] = row[qd + kvd + idx];
+    }
+}
+
+// Row (t, h) of S (keys 0..L-1, padded to lp): p = exp(s - peak) / total over keys
+// 0..first+t with s = S / sqrt(head_dim); masked and padding keys get 0.
+__global__ __launch_bounds__(256) void attn_softmax_batch_kernel(AttnBatchArgs a) {
+    __shared__ float red[8];
+    const int row = blockIdx.x;  // h * count + t
+    const int t = row % a.count;
+    const int n = a.first + t + 1;
+    float* s = a.scores + (size_t)row * a.lp;
+    const float root = sqrtf((float)a.head_dim);
+    float m = -INFINITY;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) m = fmaxf(m, s[j] / root);
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float total = 0.f;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+        const float e = expf(s[j] / root - m);
+        s[j] = e;
+        total += e;
+    }
+    total = wave_sum(total);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = total;
+    __syncthreads();
+    total = (red[0] + red[1]) + (red[2] + red[3]);
+    for (int j = threadIdx.x; j < a.lp; j += blockDim.x) s[j] = j < n ? s[j] / total : 0.f;
+}
+
+// vt[kvh][d][j] = values[j][kvh][d] for keys j < L, 0 up to lp: 32 x 32 tiles via LDS.
+__global__ __launch_bounds__(256) void attn_vt_batch_kernel(AttnBatchArgs a) {
+    __shared__ float tile[32][33];
+    const int kvh = blockIdx.z, d0 = blockIdx.y * 32, j0 = blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    const int L = a.first + a.count, kvd = a.kv_heads * a.head_dim;
+    for (int r = ty; r < 32; r += 8) {
+        const int j = j0 + r;
+        tile[r][tx] = j < L ? a.values[(size_t)j * kvd + (size_t)kvh * a.head_dim + d0 + tx] : 0.f;
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8)
+        a.vt[((size_t)kvh * a.head_dim + d0 + r) * a.lp + j0 + tx] = tile[tx][r];
+}
+
+// out[t][h*hd + d] = o[t][h*hd + d] * sigmoid(gate) (model.cpp:153)
+__global__ __launch_bounds__(256) void attn_gate_batch_kernel(AttnBatchArgs a) {
+    const int hdim = a.heads * a.head_dim;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)a.count * hdim) return;
+    const int t = (int)(i / hdim), c = (int)(i % hdim), h = c / a.head_dim, d = c % a.head_dim;
+    const float g = a.qkv[(size_t)t * a.stride + (size_t)h * a.head_dim * 2 + a.head_dim + d];
+    a.out[(size_t)t * a.out_stride + c] = a.o[i] * sigmoidf_(g);
+}
+
 }  // namespace
+
+hipError_t launch_attention_batch(const AttnBatchArgs& a, hipStream_t stream) {
+    const int group = a.heads / a.kv_heads, hd = a.head_dim, L = a.first + a.count;
+    if (a.count < 1 || a.heads % a.kv_heads || a.lp % 32 || a.lp < L || hd % 32) return hipErrorInvalidValue;
+    const size_t prep_lds = (size_t)(a.heads + a.kv_heads) * hd * sizeof(float);
+    switch (hd) {
+    case 64: launch_kernel(attn_prep_batch_kernel<1>, dim3(a.count), dim3(512), prep_lds, stream, a); break;
+    case 128: launch_kernel(attn_prep_batch_kernel<2>, dim3(a.count), dim3(512), prep_lds, stream, a); break;
+    case 256: launch_kernel(attn_prep_batch_kernel<4>, dim3(a.count), dim3(512), prep_lds, stream, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int kvd = a.kv_heads * hd;
+    for (int h = 0; h < a.heads; ++h) {  // S_h = Q_h K_kvh^T
+        e = launch_gemm_f32(a.q + (size_t)h * hd, a.keys + (size_t)(h / group) * hd, a.scores + (size_t)h * a.count * a.lp,
+                            a.count, L, hd, a.heads * hd, kvd, a.lp, stream);
+        if (e != hipSuccess) return e;
+    }
+    launch_kernel(attn_softmax_batch_kernel, dim3(a.heads * a.count), dim3(256), 0, stream, a);
+    launch_kernel(attn_vt_batch_kernel, dim3(a.lp / 32, hd / 32, a.kv_heads), dim3(256), 0, stream, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    for (int h = 0; h < a.heads; ++h) {  // O_h = P_h V_kvh
+        e = launch_gemm_f32(a.scores + (size_t)h * a.count * a.lp, a.vt + (size_t)(h / group) * hd * a.lp,
+                            a.o + (size_t)h * hd, a.count, hd, a.lp, a.lp, a.lp, a.heads * hd, stream);
+        if (e != hipSuccess) return e;
+    }
+    const size_t n = (size_t)a.count * a.heads * hd;
+    launch_kernel(attn_gate_batch_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
 
 size_t attention_partial_floats(int heads, int kv_heads, int head_dim, int context) {
     // partials of the per-op kernel (kAttnSplit ranges) or of the step program's chunks

@@ -1066,6 +1066,55 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
     return run_matvec(h, &po, 1, kMvPlain, nullptr, dn, nullptr, nullptr, 0, nullptr);
 }
 
+emprise_status emprise_hip_attention_batch(emprise_hip* h, const emprise_hip_attention_params* p, emprise_dev qkv,
+                                           int count, uint64_t stride, int first_position, emprise_dev out,
+                                           uint64_t out_stride) {
+    if (!h || !p || !qkv || !out || !p->keys || !p->values) return fail(EMPRISE_EINVAL, "null argument");
+    const Weight *qn = h->weight(p->q_norm), *kn = h->weight(p->k_norm);
+    if (p->heads < 1 || p->kv_heads < 1 || p->heads % p->kv_heads ||
+        (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256) || p->rotary > p->head_dim || p->rotary % 2 ||
+        p->rotary < 0 || p->context < 1 || !qn || !kn || qn->type != kF32 || kn->type != kF32 ||
+        qn->rows * qn->cols != (uint64_t)p->head_dim || kn->rows * kn->cols != (uint64_t)p->head_dim)
+        return fail(EMPRISE_EINVAL, "Attention projection dimensions");
+    const uint64_t qkv_w = (uint64_t)p->heads * p->head_dim * 2 + 2 * (uint64_t)p->kv_heads * p->head_dim;
+    if (count < 1 || first_position < 0 || (int64_t)first_position + count > p->context || stride < qkv_w ||
+        out_stride < (uint64_t)p->heads * p->head_dim)
+        return fail(EMPRISE_EINVAL, "attention_batch: positions %d..%d of a %d-position context, stride %llu",
+                    first_position, first_position + count - 1, p->context, (unsigned long long)stride);
+    if (h->recording) return rec_unsupported(h, "batched attention");
+    AttnBatchArgs a{};
+    a.heads = p->heads;
+    a.kv_heads = p->kv_heads;
+    a.head_dim = p->head_dim;
+    a.rotary = p->rotary;
+    a.count = count;
+    a.first = first_position;
+    a.lp = (first_position + count + 31) / 32 * 32;
+    a.eps = p->eps;
+    a.rope_base = p->rope_base;
+    a.q_norm = reinterpret_cast<const float*>(qn->dev);
+    a.k_norm = reinterpret_cast<const float*>(kn->dev);
+    a.qkv = reinterpret_cast<const float*>(qkv);
+    a.stride = stride;
+    a.keys = reinterpret_cast<float*>(p->keys);
+    a.values = reinterpret_cast<float*>(p->values);
+    a.out = reinterpret_cast<float*>(out);
+    a.out_stride = out_stride;
+    const size_t hq = (size_t)count * p->heads * p->head_dim;
+    void *q, *sc, *vt, *o;
+    TRY(h->get_scratch("attnb_q", hq * sizeof(float), &q));
+    TRY(h->get_scratch("attnb_s", (size_t)p->heads * count * a.lp * sizeof(float), &sc));
+    TRY(h->get_scratch("attnb_vt", (size_t)p->kv_heads * p->head_dim * a.lp * sizeof(float), &vt));
+    TRY(h->get_scratch("attnb_o", hq * sizeof(float), &o));
+    a.q = static_cast<float*>(q);
+    a.scores = static_cast<float*>(sc);
+    a.vt = static_cast<float*>(vt);
+    a.o = static_cast<float*>(o);
+    // K/V rows 0..first+count-1 read twice (scores, transpose), the new rows written
+    const uint64_t bytes = 3 * (uint64_t)(first_position + count) * p->kv_heads * p->head_dim * 4 + count * qkv_w * 4;
+    return traced(h, "attention_batch", bytes, [&] { return launch_attention_batch(a, h->stream); });
+}
+
 emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention_params* p, emprise_dev qkv,
                                      emprise_dev out) {
     if (!h || !p || !qkv || !out || !p->keys || !p->values || !p->position) return fail(EMPRISE_EINVAL, "null argument");

@@ -147,6 +147,27 @@ struct AttnArgs {
 constexpr int kAttnChunk = 64;    // positions per partial of the step program's attention
 constexpr int kAttnSub = 16;     // positions per step of attention_kernel's online softmax
 constexpr int kAttnSplit = 64;   // position ranges (workgroups) per KV head of attention_kernel
+// `count` consecutive prompt positions from absolute position `first`: qkv row t at
+// t * stride floats; q (count x heads x hd), scores (heads x count x lp), vt (kv_heads x
+// hd x lp) and o (count x heads x hd) are scratch, lp = first + count rounded up to 32;
+// out row t at t * out_stride.
+struct AttnBatchArgs {
+    int heads, kv_heads, head_dim, rotary, count, first, lp;
+    float eps, rope_base;
+    const float* q_norm;
+    const float* k_norm;
+    const float* qkv;
+    size_t stride;
+    float* keys;
+    float* values;
+    float* q;
+    float* scores;
+    float* vt;
+    float* o;
+    float* out;
+    size_t out_stride;
+};
+hipError_t launch_attention_batch(const AttnBatchArgs& a, hipStream_t stream);
 size_t attention_partial_floats(int heads, int kv_heads, int head_dim, int context);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 

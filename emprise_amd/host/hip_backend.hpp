@@ -62,6 +62,10 @@ public:
     void dev_attention(const emprise_hip_attention_params& p, emprise_dev qkv, emprise_dev out) {
         hip_check(emprise_hip_attention(h_, &p, qkv, out), "attention");
     }
+    void dev_attention_batch(const emprise_hip_attention_params& p, emprise_dev qkv, int count, uint64_t stride,
+                             int first, emprise_dev out, uint64_t out_stride) {
+        hip_check(emprise_hip_attention_batch(h_, &p, qkv, count, stride, first, out, out_stride), "attention_batch");
+    }
     void dev_embed(emprise_weight w, emprise_dev token, emprise_dev out) { hip_check(emprise_hip_embed(h_, w, token, out), "embed"); }
     void dev_embed_rows(emprise_weight w, emprise_dev tokens, int count, emprise_dev out) {
         hip_check(emprise_hip_embed_rows(h_, w, tokens, count, out), "embed_rows");

@@ -394,9 +394,9 @@ std::vector<float> Model::last_hidden() {
 // tokens: every projection runs once per chunk as a GEMM on the matrix cores (the
 // reference batches 4 positions, model.cpp:355-366; here the whole chunk), the RMSNorms,
 // residual adds and SwiGLU run over all rows at once, the GDN conv + state update runs
-// as one scan over the chunk's positions (emprise_hip_delta_net_batch), and attention,
-// which reads the K/V rows the previous positions appended, runs per position on the
-// decode kernels. Op order and arithmetic are those of the unfused decode step.
+// as one scan over the chunk's positions (emprise_hip_delta_net_batch), and attention
+// runs over the chunk at once as FP32 GEMMs with a causal softmax
+// (emprise_hip_attention_batch). Op order is that of the unfused decode step.
 void Model::prefill_batched(size_t count) {
     constexpr size_t kPrefillChunk = 2048;
     HipBackend& b = *backend_;
@@ -408,21 +408,17 @@ void Model::prefill_batched(size_t count) {
     const uint64_t wa = std::max({ch + vd + 2 * vh, qd + 2 * kvd, F}), wb = std::max({vd, ao, F});
     const size_t rows = std::min(count, kPrefillChunk);
     if (pf_rows_ < rows) {
-        for (emprise_dev* p : {&pf_x_, &pf_xn_, &pf_a_, &pf_b_, &pf_c_, &pf_pos_})
+        for (emprise_dev* p : {&pf_x_, &pf_xn_, &pf_a_, &pf_b_, &pf_c_})
             if (*p) b.dev_free(*p), *p = 0;
         pf_x_ = b.dev_alloc(rows * H * 4);
         pf_xn_ = b.dev_alloc(rows * H * 4);
         pf_a_ = b.dev_alloc(rows * wa * 4);
         pf_b_ = b.dev_alloc(rows * wb * 4);
         pf_c_ = b.dev_alloc(rows * H * 4);
-        pf_pos_ = b.dev_alloc(rows * sizeof(int));
         pf_rows_ = rows;
     }
-    std::vector<int> pos(rows);
     for (size_t p0 = 0; p0 < count; p0 += rows) {
         const int T = static_cast<int>(std::min(rows, count - p0));
-        for (int t = 0; t < T; ++t) pos[t] = static_cast<int>(p0) + t;
-        b.dev_upload(pf_pos_, pos.data(), T * sizeof(int));
         b.dev_embed_rows(embd_, dev_prompt_ + p0 * sizeof(int), T, pf_x_);
         for (const Layer& L : layers_) {
             b.dev_rmsnorm_rows(pf_x_, L.attn_norm, pf_xn_, static_cast<int>(H), T, d.eps);
@@ -468,10 +464,7 @@ void Model::prefill_batched(size_t count) {
                 p.k_norm = L.k_norm;
                 p.keys = L.keys;
                 p.values = L.values;
-                for (int t = 0; t < T; ++t) {
-                    p.position = pf_pos_ + uint64_t(t) * sizeof(int);
-                    b.dev_attention(p, pf_a_ + uint64_t(t) * W * 4, pf_b_ + uint64_t(t) * ao * 4);
-                }
+                b.dev_attention_batch(p, pf_a_, T, W, static_cast<int>(p0), pf_b_, ao);
                 b.dev_linear_batch(L.o, pf_b_, ao, pf_c_, H, T);
             }
             b.dev_add(pf_x_, pf_c_, static_cast<int>(T * H));

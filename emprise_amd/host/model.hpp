@@ -73,7 +73,7 @@ private:
     emprise_graph graph_full_ = 0, graph_prefill_ = 0;
     // batched prefill buffers, sized for pf_rows_ tokens on first use
     size_t pf_rows_ = 0;
-    emprise_dev pf_x_ = 0, pf_xn_ = 0, pf_a_ = 0, pf_b_ = 0, pf_c_ = 0, pf_d_ = 0, pf_pos_ = 0;
+    emprise_dev pf_x_ = 0, pf_xn_ = 0, pf_a_ = 0, pf_b_ = 0, pf_c_ = 0;
     bool have_graph_full_ = false, have_graph_prefill_ = false;
     int step_program_ = -1;  // 1: step graphs are persistent programs, 0: per-op graphs, -1: none yet
 

@@ -221,6 +221,17 @@ typedef struct {
 } emprise_hip_attention_params;
 emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention_params* p, emprise_dev qkv,
                                      emprise_dev out);
+/* attention_preout over `count` consecutive prompt positions first_position .. +count-1
+ * (the reference attends position by position inside its 4-position prefill batches,
+ * model.cpp:355-366): qkv is the row of the first position, the rows of later positions
+ * `stride` floats further; their k/v are appended to the caches at their positions and
+ * position t attends over 0..first_position+t; out receives `count` rows `out_stride`
+ * floats apart. p->position is not used. The dot products and P.V run as FP32 GEMMs on
+ * the matrix cores, so the outputs equal those of `count` emprise_hip_attention calls
+ * up to summation order. */
+emprise_status emprise_hip_attention_batch(emprise_hip* h, const emprise_hip_attention_params* p, emprise_dev qkv,
+                                           int count, uint64_t stride, int first_position, emprise_dev out,
+                                           uint64_t out_stride);
 
 /* ---- state, sync, graphs ---------------------------------------------------------- */
 /* Backend::reset_state (backend.hpp:53). The caller owns recurrent and KV state buffers

@@ -326,6 +326,57 @@ def test_attention_tiny(backend, L):
     _attention_case(backend, 8, 2, 64, 16, L, 512, seed=100 + L)
 
 
+@pytest.mark.parametrize("heads,kv,hd,rot,first,count,context", [(16, 4, 256, 64, 0, 40, 4096),
+                                                                (16, 4, 256, 64, 100, 37, 4096),
+                                                                (8, 2, 64, 16, 0, 130, 512), (8, 2, 64, 16, 5, 1, 512)])
+def test_attention_batch_matches_steps(backend, heads, kv, hd, rot, first, count, context):
+    """emprise_hip_attention_batch over positions first..first+count-1 (strided qkv rows,
+    caches holding `first` earlier rows) against `count` decode attention calls on a copy
+    of the caches: outputs within the per-op bar (GEMM summation order), appended K/V rows
+    equal; two outputs also against the oracle."""
+    rng = np.random.default_rng(3 + first + count)
+    kvd, qd = kv * hd, heads * hd * 2
+    W = qd + 2 * kvd + 4
+    qn = (1 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+    keys = np.zeros((context, kvd), np.float32)
+    values = np.zeros((context, kvd), np.float32)
+    keys[:first] = rng.standard_normal((first, kvd)).astype(np.float32)
+    values[:first] = rng.standard_normal((first, kvd)).astype(np.float32)
+    rows = rng.standard_normal((count, W)).astype(np.float32)
+    qnv, knv = backend.vector(qn), backend.vector(kn)
+    # position by position
+    ks, vs = backend.to_device(keys), backend.to_device(values)
+    qkv1, pos, out1 = backend.alloc(W * 4), backend.alloc(4), backend.alloc(heads * hd * 4)
+    seq = np.zeros((count, heads * hd), np.float32)
+    for t in range(count):
+        backend.upload(qkv1, rows[t])
+        backend.upload(pos, np.array([first + t], np.int32))
+        p = AttentionParams(heads, kv, hd, rot, context, 1e-6, 1e7, qnv, knv, ks, vs, pos)
+        backend.attention(p, qkv1, out1)
+        seq[t] = backend.download(out1, heads * hd)
+    # batched
+    kb, vb = backend.to_device(keys), backend.to_device(values)
+    rows_d = backend.to_device(rows)
+    out_stride = heads * hd + 8
+    ob = backend.alloc(count * out_stride * 4)
+    p = AttentionParams(heads, kv, hd, rot, context, 1e-6, 1e7, qnv, knv, kb, vb, 0)
+    backend.attention_batch(p, rows_d, count, W, first, ob, out_stride)
+    got = backend.download(ob, count * out_stride).reshape(count, out_stride)[:, :heads * hd]
+    for t in range(count):
+        _close(got[t], seq[t], what=f"position {first + t}")
+    n = first + count
+    _close(backend.download(kb, (context, kvd))[:n], backend.download(ks, (context, kvd))[:n], what="keys")
+    assert np.array_equal(backend.download(vb, (context, kvd))[:n], backend.download(vs, (context, kvd))[:n])
+    for t in (0, count - 1):
+        r = rows[t]
+        kc = backend.download(kb, (context, kvd)).copy()
+        vc = backend.download(vb, (context, kvd)).copy()
+        ref = oracle.attention(heads, kv, hd, rot, 1e7, 1e-6, qn, kn, r[:qd], r[qd:qd + kvd], r[qd + kvd:qd + 2 * kvd],
+                               kc, vc, first + t + 1, first + t)
+        _close(got[t], ref, what=f"position {first + t} vs oracle")
+
+
 def test_attention_rejects_bad_shape(backend):
     p = AttentionParams(16, 5, 256, 64, 64, 1e-6, 1e7, backend.vector(np.ones(256, np.float32)),
                         backend.vector(np.ones(256, np.float32)), 1, 1, 1)
