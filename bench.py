@@ -149,6 +149,27 @@ def attention_probe(kv_len: int, calls: int = 40):
     log(f"{calls} attention calls at {kv_len} positions")
 
 
+def gemm_probe(tokens: int, calls: int = 10):
+    """Batched projection of `tokens` positions through a 12288 x 4096 Q6_K matrix (the
+    9B FFN gate shape) -- the prefill GEMM (dequantised FP32 rows on the matrix cores) --
+    `calls` times, for profilers; seeded synthetic weights and inputs."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "tests"))
+    from synth import matrix
+    import emprise_amd as ea
+    be = ea.HipBackend(0)
+    rng = np.random.default_rng(5)
+    rows, cols = 12288, 4096
+    w = be.upload_weight(ea.Q6_K, cols, rows, matrix(rng, ea.Q6_K, rows, cols))
+    x = be.to_device(rng.standard_normal((tokens, cols)).astype(np.float32))
+    y = be.alloc(tokens * rows * 4)
+    for _ in range(calls):
+        be.linear_batch(w, x, y, tokens)
+    be.sync()
+    be.close()
+    log(f"{calls} batched projections of {tokens} tokens through {rows} x {cols} Q6_K")
+
+
 def _graph_time_ms(be, fn, n=20, reps=5):
     """Mean duration of `fn`'s launches, replayed n times per graph, reps graphs."""
     fn()
@@ -279,6 +300,8 @@ def main():
                     help="only run a device-to-device copy of MIB MiB (counter calibration) and exit")
     ap.add_argument("--attention-probe", type=int, metavar="KV_LEN",
                     help="only run 40 eager 9B-shape attention calls over KV_LEN positions (for profilers) and exit")
+    ap.add_argument("--gemm-probe", type=int, metavar="TOKENS",
+                    help="only run 10 batched 12288x4096 Q6_K projections of TOKENS positions (for profilers) and exit")
     ap.add_argument("--suite", action="store_true",
                     help="only run the other benchmark configurations (C1, C2, C4), one JSON line each")
     args = ap.parse_args()
@@ -288,6 +311,9 @@ def main():
         sys.exit(2)
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.gemm_probe:
+        gemm_probe(args.gemm_probe)
         return
     if args.attention_probe:
         attention_probe(args.attention_probe)
