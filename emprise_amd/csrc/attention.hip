@@ -38,7 +38,6 @@ namespace {
 
 constexpr int kAttnWaves = 8;
 constexpr int kMaxGroup = 8;
-constexpr int kCombineMaxChunks = kAttnSplit;
 
 // E consecutive floats (lane l of a wave owns dims E*l .. E*l+E-1 of a head): one
 // 16-, 8- or 4-byte access.
@@ -285,54 +284,43 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     }
 }
 
-// Merges the chunk partials of one query head and 64 of its output dims:
+// Merges the range partials of one query head and 64 of its output dims:
 // o = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, then the sigmoid output gate
-// (model.cpp:153). Every load (chunk statistics and the wave's share of the chunks'
-// o values) is issued once the position is known, before any arithmetic; wave w sums
-// chunks w, w+4, ... and the four waves' sums are added through LDS.
-constexpr int kCombineBatch = 16;  // chunks per wave held in registers per pass
+// (model.cpp:153). There are at most kAttnSplit partials, so every load -- the gate,
+// each wave's share of the o values (ranges w, w+4, ...), the statistics -- goes out
+// together with the position's, before it is known which ranges hold positions (the
+// slots of the others are loaded but never used); the four waves' sums are added
+// through LDS.
+constexpr int kCombineBatch = kAttnSplit / 4;  // ranges per wave
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
-    __shared__ float wts[kCombineMaxChunks];
+    __shared__ float wts[kAttnSplit];
     __shared__ float red[8];
     __shared__ float part[4][64];
     const int hd = a.head_dim, group = a.heads / a.kv_heads, dblocks = hd / 64;
     const int head = blockIdx.x / dblocks, db = blockIdx.x - head * dblocks;
-    const int pos = *a.position;
-    if (pos < 0 || pos >= a.context) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunks_max = kAttnSplit;
-    const int nsub = pos / kAttnSub + 1, per = attn_per(pos + 1);
-    const int nchunks = (nsub + per - 1) / per;  // ranges holding positions
     const int kvh = head / group, g = head - kvh * group, stride = hd + 2;
-    const float* base = a.partial + ((size_t)kvh * chunks_max * group + g) * stride;
+    const float* base = a.partial + ((size_t)kvh * kAttnSplit * group + g) * stride;
     const size_t cstride = (size_t)group * stride;
     const int d = db * 64 + lane;
-
-    // the gate, the first pass of o values and the statistics, all in flight together
+    const int pos = *a.position;
     const float gate = a.qkv[(size_t)head * hd * 2 + hd + d];
     float ov[kCombineBatch];
 #pragma unroll
-    for (int i = 0; i < kCombineBatch; ++i) {
-        const int c = min(wave + 4 * i, nchunks - 1);
-        ov[i] = base[(size_t)c * cstride + d];
-    }
-    float mloc = -INFINITY;
-    for (int c = threadIdx.x; c < nchunks; c += blockDim.x) {
-        const float m = base[(size_t)c * cstride + hd];
-        wts[c] = m;
-        mloc = fmaxf(mloc, m);
-    }
-    mloc = wave_max(mloc);
+    for (int i = 0; i < kCombineBatch; ++i) ov[i] = base[(size_t)(wave + 4 * i) * cstride + d];
+    const int cs = min((int)threadIdx.x, kAttnSplit - 1);
+    const float m_c = base[(size_t)cs * cstride + hd], l_c = base[(size_t)cs * cstride + hd + 1];
+    if (pos < 0 || pos >= a.context) return;
+    const int nsub = pos / kAttnSub + 1, per = attn_per(pos + 1);
+    const int nchunks = (nsub + per - 1) / per;  // ranges holding positions
+    const bool own = (int)threadIdx.x < nchunks;
+    const float mloc = wave_max(own ? m_c : -INFINITY);
     if (lane == 0) red[wave] = mloc;
     lds_barrier();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float dloc = 0.f;
-    for (int c = threadIdx.x; c < nchunks; c += blockDim.x) {
-        const float w = expf(wts[c] - M);
-        wts[c] = w;
-        dloc = fmaf(w, base[(size_t)c * cstride + hd + 1], dloc);
-    }
-    dloc = wave_sum(dloc);
+    const float w = own ? expf(m_c - M) : 0.f;
+    if ((int)threadIdx.x < kAttnSplit) wts[threadIdx.x] = w;
+    const float dloc = wave_sum(own ? w * l_c : 0.f);
     lds_barrier();  // every weight is in wts; red is free again
     if (lane == 0) red[4 + wave] = dloc;
     float num = 0.f;
@@ -340,13 +328,6 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
     for (int i = 0; i < kCombineBatch; ++i) {
         const int c = wave + 4 * i;
         if (c < nchunks) num = fmaf(wts[c], ov[i], num);
-    }
-    for (int c0 = wave + 4 * kCombineBatch; c0 < nchunks; c0 += 4 * kCombineBatch) {  // long contexts
-#pragma unroll
-        for (int i = 0; i < kCombineBatch; ++i) ov[i] = base[(size_t)min(c0 + 4 * i, nchunks - 1) * cstride + d];
-#pragma unroll
-        for (int i = 0; i < kCombineBatch; ++i)
-            if (c0 + 4 * i < nchunks) num = fmaf(wts[c0 + 4 * i], ov[i], num);
     }
     part[wave][lane] = num;
     lds_barrier();
