@@ -761,47 +761,84 @@ emprise_status emprise_hip_linear_batch(emprise_hip* h, emprise_weight w, empris
     return emprise_hip_linear_batch_strided(h, w, X, wt->cols, Y, wt->rows, K);
 }
 
+// Y[k] = [W_0; W_1; ...] X[k]: the weights' rows side by side in Y, for K rows of X. From
+// kGemmMinBatch rows up the quantised rows are dequantised exactly into a scratch block
+// (weight by weight, each into its rows of the block) and the block runs as one GEMM, so
+// the weights of one input (q|k|v, the recurrent in-projections) share one launch and
+// its full tiles; below that, the streaming matvec per row of X.
+static emprise_status linear_batch_rows(emprise_hip* h, int nw, const Weight* const* ws, emprise_dev X, uint64_t ldx,
+                                        emprise_dev Y, uint64_t ldy, int K) {
+    const int cols = (int)ws[0]->cols;
+    uint64_t rows = 0;
+    bool all_f32 = true;
+    for (int i = 0; i < nw; ++i) rows += ws[i]->rows, all_f32 = all_f32 && ws[i]->type == kF32;
+    if (ldx < (uint64_t)cols || ldy < rows || ldx > (1u << 30) || ldy > (1u << 30))
+        return fail(EMPRISE_EINVAL, "row strides shorter than the matrix");
+    if (K < kGemmMinBatch || cols % 16 != 0 || X % 16 != 0 || ldx % 4 != 0) {
+        uint64_t off = 0;
+        for (int i = 0; i < nw; ++i) {
+            for (int k = 0; k < K; ++k) {
+                Proj p{ws[i], reinterpret_cast<float*>(Y) + (size_t)k * ldy + off};
+                TRY(run_matvec(h, &p, 1, kMvPlain, nullptr, reinterpret_cast<const float*>(X) + (size_t)k * ldx,
+                               nullptr, nullptr, 0, nullptr));
+            }
+            off += ws[i]->rows;
+        }
+        return EMPRISE_OK;
+    }
+    const float* A = reinterpret_cast<const float*>(X);
+    float* C = reinterpret_cast<float*>(Y);
+    const uint64_t flops_per_row = 2ull * (uint64_t)K * (uint64_t)cols;
+    if (nw == 1 && all_f32) {
+        return traced(h, "gemm_f32", flops_per_row * rows, [&] {
+            return launch_gemm_f32(A, reinterpret_cast<const float*>(ws[0]->dev), C, K, (int)rows, cols, (int)ldx,
+                                   cols, (int)ldy, h->stream);
+        });
+    }
+    // dequantise (or copy, for F32 rows) blocks of the stacked rows to FP32 (exact), then
+    // multiply
+    const uint64_t block = std::max<uint64_t>(128, kGemmScratchBytes / ((uint64_t)cols * 4) / 128 * 128);
+    const uint64_t nb = std::min<uint64_t>(block, rows);
+    void* wf;
+    TRY(h->get_scratch("gemm_w", nb * cols * sizeof(float), &wf));
+    for (uint64_t r0 = 0; r0 < rows; r0 += nb) {
+        const uint64_t n = std::min<uint64_t>(nb, rows - r0);
+        uint64_t first = 0;  // stacked index of weight i's row 0
+        for (int i = 0; i < nw; ++i) {
+            const Weight* wt = ws[i];
+            const uint64_t lo = std::max(first, r0), hi = std::min(first + wt->rows, r0 + n);
+            if (lo < hi) {
+                float* dst = static_cast<float*>(wf) + (lo - r0) * cols;
+                TRY(traced(h, "dequant_rows", (hi - lo) * (wt->bytes / wt->rows + (uint64_t)cols * 4), [&] {
+                    return launch_dequant_rows(wt->dev, wt->type, cols, lo - first, hi - lo, dst, h->stream);
+                }));
+            }
+            first += wt->rows;
+        }
+        TRY(traced(h, "gemm_f32", flops_per_row * n, [&] {
+            return launch_gemm_f32(A, static_cast<const float*>(wf), C + r0, K, (int)n, cols, (int)ldx, cols, (int)ldy,
+                                   h->stream);
+        }));
+    }
+    return EMPRISE_OK;
+}
+
 emprise_status emprise_hip_linear_batch_strided(emprise_hip* h, emprise_weight w, emprise_dev X, uint64_t ldx,
                                                 emprise_dev Y, uint64_t ldy, int K) {
     if (!h || !X || !Y || K < 1) return fail(EMPRISE_EINVAL, "bad arguments");
     const Weight* wt;
     TRY(check_weights(h, 1, &w, &wt));
-    const int cols = (int)wt->cols, rows = (int)wt->rows;
-    if (ldx < wt->cols || ldy < wt->rows || ldx > (1u << 30) || ldy > (1u << 30))
-        return fail(EMPRISE_EINVAL, "row strides shorter than the matrix");
-    if (K >= kGemmMinBatch && cols % 16 == 0 && X % 16 == 0 && ldx % 4 == 0) {
-        const float* A = reinterpret_cast<const float*>(X);
-        float* C = reinterpret_cast<float*>(Y);
-        const uint64_t flops_per_row = 2ull * (uint64_t)K * (uint64_t)cols;
-        if (wt->type == kF32) {
-            return traced(h, "gemm_f32", flops_per_row * rows, [&] {
-                return launch_gemm_f32(A, reinterpret_cast<const float*>(wt->dev), C, K, rows, cols, (int)ldx, cols,
-                                       (int)ldy, h->stream);
-            });
-        }
-        // quantised weights: dequantise a block of rows to FP32 (exact), then multiply
-        const uint64_t block = std::max<uint64_t>(128, kGemmScratchBytes / ((uint64_t)cols * 4) / 128 * 128);
-        const uint64_t nb = std::min<uint64_t>(block, (uint64_t)rows);
-        void* wf;
-        TRY(h->get_scratch("gemm_w", nb * cols * sizeof(float), &wf));
-        for (uint64_t r0 = 0; r0 < (uint64_t)rows; r0 += nb) {
-            const uint64_t n = std::min<uint64_t>(nb, rows - r0);
-            TRY(traced(h, "dequant_rows", n * wt->bytes / rows + n * cols * 4, [&] {
-                return launch_dequant_rows(wt->dev, wt->type, cols, r0, n, static_cast<float*>(wf), h->stream);
-            }));
-            TRY(traced(h, "gemm_f32", flops_per_row * n, [&] {
-                return launch_gemm_f32(A, static_cast<const float*>(wf), C + r0, K, (int)n, cols, (int)ldx, cols,
-                                       (int)ldy, h->stream);
-            }));
-        }
-        return EMPRISE_OK;
-    }
-    for (int k = 0; k < K; ++k) {
-        Proj p{wt, reinterpret_cast<float*>(Y) + (size_t)k * ldy};
-        TRY(run_matvec(h, &p, 1, kMvPlain, nullptr, reinterpret_cast<const float*>(X) + (size_t)k * ldx, nullptr,
-                       nullptr, 0, nullptr));
-    }
-    return EMPRISE_OK;
+    return linear_batch_rows(h, 1, &wt, X, ldx, Y, ldy, K);
+}
+
+emprise_status emprise_hip_linear_batch_many(emprise_hip* h, int n, const emprise_weight* w, emprise_dev X,
+                                             uint64_t ldx, emprise_dev Y, uint64_t ldy, int K) {
+    if (!h || !w || !X || !Y || K < 1 || n < 1 || n > kMaxSeg) return fail(EMPRISE_EINVAL, "bad arguments");
+    const Weight* ws[kMaxSeg];
+    TRY(check_weights(h, n, w, ws));
+    for (int i = 1; i < n; ++i)
+        if (ws[i]->cols != ws[0]->cols) return fail(EMPRISE_EINVAL, "linear_batch_many: input widths differ");
+    return linear_batch_rows(h, n, ws, X, ldx, Y, ldy, K);
 }
 
 emprise_status emprise_hip_ffn_gate_up(emprise_hip* h, const emprise_hip_input* in, emprise_dev x, emprise_weight gate,
@@ -953,13 +990,15 @@ emprise_status emprise_hip_delta_net_batch(emprise_hip* h, const emprise_hip_del
         return fail(EMPRISE_EINVAL, "Recurrent projection dimensions");
     if (!p->qkv || !p->gate || !p->alpha || !p->beta || !p->conv_state || !p->rec_state || !p->out)
         return fail(EMPRISE_EINVAL, "null buffer");
-    if (count < 1 || stride < (uint64_t)ch || out_stride < (uint64_t)vd)
+    if (count < 1 || count > (1 << 19) || stride < (uint64_t)ch || out_stride < (uint64_t)vd)
         return fail(EMPRISE_EINVAL, "delta_net_batch: count %d, stride %llu, out_stride %llu", count,
                     (unsigned long long)stride, (unsigned long long)out_stride);
     if (h->recording) return rec_unsupported(h, "batched delta_net");
-    void *conv_out, *o;
+    void *conv_out, *o, *qk, *gates;
     TRY(h->get_scratch("gdn_conv_batch", (size_t)count * ch * sizeof(float), &conv_out));
     TRY(h->get_scratch("gdn_o_batch", (size_t)count * vd * sizeof(float), &o));
+    TRY(h->get_scratch("gdn_qk_batch", (size_t)count * 2 * kd * sizeof(float), &qk));
+    TRY(h->get_scratch("gdn_gates_batch", (size_t)count * 2 * p->value_heads * sizeof(float), &gates));
     GdnBatchArgs g{};
     g.key_heads = p->key_heads;
     g.value_heads = p->value_heads;
@@ -979,6 +1018,8 @@ emprise_status emprise_hip_delta_net_batch(emprise_hip* h, const emprise_hip_del
     g.conv_state = reinterpret_cast<float*>(p->conv_state);
     g.state = reinterpret_cast<float*>(p->rec_state);
     g.conv_out = static_cast<float*>(conv_out);
+    g.qk = static_cast<float*>(qk);
+    g.gates = static_cast<float*>(gates);
     g.o = static_cast<float*>(o);
     g.out = reinterpret_cast<float*>(p->out);
     g.out_stride = out_stride;

@@ -16,6 +16,14 @@ __device__ __forceinline__ void q4_scale_min(const uint8_t* s, int j, int& sc, i
     }
 }
 
+// The element formulas of dequantize() (quant.cpp:25-61), shared by every decoder so
+// each forms the value with the same operations in the same order: Q6_K (d*sc)*(q-32),
+// Q4_K (d*sc)*q - dmin*m.
+__device__ __forceinline__ float q6k_weight(float d, int8_t sc, int code) { return d * (float)sc * (float)(code - 32); }
+__device__ __forceinline__ float q4k_weight(float dd, float dm, int sc, int mn, int code) {
+    return (dd * (float)sc) * (float)code - dm * (float)mn;
+}
+
 // Weight (row r, column k) of a matrix with `cols` inputs, exactly as the CPU
 // dequantize() produces it (quant.cpp:25-78): the Q6_K product (d*sc)*q and the Q4_K
 // (d*sc)*q - dmin*m are formed in the same order.
@@ -32,8 +40,7 @@ __device__ __forceinline__ float decode_element(const uint8_t* w, uint32_t type,
             code = (ch[4 * u + b] >> 6) | ((ch[1024 + 4 * u + b] >> 6) << 2) | ((ch[2048 + 4 * u + b] >> 6) << 4);
         }
         const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(ch + 3328 + 2 * (u >> 4)));
-        const float sc = (float)(int8_t)ch[3072 + u];
-        return d * sc * (float)(code - 32);
+        return q6k_weight(d, (int8_t)ch[3072 + u], code);
     }
     if (type == kQ4K && cols % kChunkCols == 0) {
         const uint8_t* ch = w + r * (uint64_t)nb * 144 + (size_t)(k / kChunkCols) * 2304;
@@ -46,7 +53,7 @@ __device__ __forceinline__ float decode_element(const uint8_t* w, uint32_t type,
         const uint8_t* dp = ch + 2240 + 4 * (u >> 3);
         const float dd = half_bits_to_float(*reinterpret_cast<const uint16_t*>(dp));
         const float dm = half_bits_to_float(*reinterpret_cast<const uint16_t*>(dp + 2));
-        return (dd * (float)sc) * (float)code - dm * (float)mn;
+        return q4k_weight(dd, dm, sc, mn, code);
     }
     if (type == kQ6K) {
         const uint8_t* row = w + r * (uint64_t)nb * 210;
@@ -56,8 +63,7 @@ __device__ __forceinline__ float decode_element(const uint8_t* w, uint32_t type,
         if (t < 12) code = q[t] & 63;
         else code = (q[t - 12] >> 6) | ((q[t - 8] >> 6) << 2) | ((q[t - 4] >> 6) << 4);
         const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(row + (size_t)nb * 208 + 2 * (u >> 4)));
-        const float sc = (float)(int8_t)row[(size_t)nb * 192 + u];
-        return d * sc * (float)(code - 32);
+        return q6k_weight(d, (int8_t)row[(size_t)nb * 192 + u], code);
     }
     if (type == kQ4K) {
         const uint8_t* row = w + r * (uint64_t)nb * 144;
@@ -69,7 +75,7 @@ __device__ __forceinline__ float decode_element(const uint8_t* w, uint32_t type,
         const uint8_t* dp = row + (size_t)nb * 140 + (size_t)(u >> 3) * 4;
         const float dd = half_bits_to_float(*reinterpret_cast<const uint16_t*>(dp));
         const float dm = half_bits_to_float(*reinterpret_cast<const uint16_t*>(dp + 2));
-        return (dd * (float)sc) * (float)code - dm * (float)mn;
+        return q4k_weight(dd, dm, sc, mn, code);
     }
     const uint64_t i = r * (uint64_t)cols + (uint64_t)k;
     if (type == kF32) return reinterpret_cast<const float*>(w)[i];

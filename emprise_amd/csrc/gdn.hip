@@ -190,121 +190,207 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_rows_kernel(GdnArgs a) {
 // Position by position, the decode kernels above pay two launches and two dependent
 // memory round trips per position and layer. Over a prompt the three stages separate:
 // the conv1d is a scan per channel (one thread keeps a channel's history in registers
-// over all positions), the delta rule a scan per state row (one wave keeps its rows in
-// registers over all positions, the next position's q/k/v/alpha/beta loading while the
-// current one is used), and the per-head RMSNorm x SiLU(gate) is independent per
-// position. Each step does the arithmetic of delta_conv_kernel and gdn_kernel in the
+// over all positions), the delta rule a scan per state row (one wave keeps its row in
+// registers over all positions) after a parallel pass that normalises q/k and forms the
+// decay and beta gate of every position, and the per-head RMSNorm x SiLU(gate) is
+// independent per position. Each step does the arithmetic of delta_conv_kernel and gdn_kernel in the
 // same order, so the outputs and the final states are those of `count` calls of the
 // per-position path.
 
+// conv1d + SiLU of every (position, channel). Output t reads only inputs t-CW+1 .. t
+// (the ones before the prompt from the history), so the positions are independent:
+// thread = (channel, kConvSpan consecutive positions), channels across the threads of a
+// workgroup for coalesced rows. The sum runs in delta_conv_kernel's order, so the outputs
+// are its outputs bit for bit; the history moves on in delta_conv_history_kernel, once
+// every read of the old one is done.
+constexpr int kConvSpan = 8;
+
 template <int CW>
 __global__ __launch_bounds__(256) void delta_conv_batch_kernel(GdnBatchArgs a) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    constexpr int U = kConvSpan;
+    const int c = blockIdx.x * 256 + threadIdx.x, t0 = blockIdx.y * U;
+    const int ch = 2 * a.key_heads * a.state_dim + a.value_heads * a.state_dim;
+    if (c >= ch) return;
+    const float* hist = a.conv_state + (size_t)c * CW;
+    float k[CW], y[CW - 1 + U];  // y[i]: input of position t0 - (CW-1) + i
+#pragma unroll
+    for (int j = 0; j < CW; ++j) k[j] = a.conv_w[(size_t)c * CW + j];
+#pragma unroll
+    for (int i = 0; i < CW - 1; ++i) {
+        const int m = t0 - (CW - 1) + i;
+        y[i] = m >= 0 ? a.qkv[(size_t)m * a.stride + c] : hist[CW + m];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) y[CW - 1 + u] = a.qkv[(size_t)min(t0 + u, a.count - 1) * a.stride + c];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        if (t0 + u < a.count) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < CW - 1; ++j) sum += y[u + j] * k[j];
+            sum += y[u + CW - 1] * k[CW - 1];
+            a.conv_out[(size_t)(t0 + u) * ch + c] = siluf_(sum);
+        }
+    }
+}
+
+// The history after the prompt: the last CW inputs of (old history, prompt). One thread
+// per channel, ascending, so each old entry is read before its slot is overwritten.
+template <int CW>
+__global__ __launch_bounds__(256) void delta_conv_history_kernel(GdnBatchArgs a) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
     const int ch = 2 * a.key_heads * a.state_dim + a.value_heads * a.state_dim;
     if (c >= ch) return;
     float* hist = a.conv_state + (size_t)c * CW;
-    float k[CW], h[CW];
 #pragma unroll
-    for (int j = 0; j < CW; ++j) {
-        k[j] = a.conv_w[(size_t)c * CW + j];
-        h[j] = hist[j];
+    for (int i = 0; i < CW; ++i) {
+        const int m = a.count - CW + i;
+        hist[i] = m >= 0 ? a.qkv[(size_t)m * a.stride + c] : hist[CW + m];
     }
-    constexpr int U = 8;  // positions whose inputs are loaded together
-    for (int t0 = 0; t0 < a.count; t0 += U) {
-        float x[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) x[u] = a.qkv[(size_t)min(t0 + u, a.count - 1) * a.stride + c];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (t0 + u < a.count) {
-                float sum = 0.f;
-#pragma unroll
-                for (int j = 0; j < CW - 1; ++j) {
-                    const float hv = h[j + 1];
-                    h[j] = hv;
-                    sum += hv * k[j];
-                }
-                h[CW - 1] = x[u];
-                sum += x[u] * k[CW - 1];
-                a.conv_out[(size_t)(t0 + u) * ch + c] = siluf_(sum);
-            }
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < CW; ++j) hist[j] = h[j];
 }
 
-// Rows [part*SD/SPLIT, (part+1)*SD/SPLIT) of value head h over all positions; one row
-// per wave. Writes the raw outputs S.q of every position.
-template <int E, int SPLIT>
-__global__ __launch_bounds__(kGdnWaves * 64) void gdn_scan_kernel(GdnBatchArgs a) {
-    constexpr int SD = 64 * E, RPW = SD / SPLIT / kGdnWaves;
-    static_assert(RPW == 1, "one row per wave");
-    const int h = blockIdx.x / SPLIT, part = blockIdx.x - h * SPLIT, kh = h % a.key_heads;
+// The per-position inputs of the delta rule that every row of a head shares, computed
+// once per position instead of once per row: the L2-normalised q and k of each key head
+// (a wave per (position, key head), lane l keeping columns l, l+64 as gdn_kernel does, so
+// the sums and scales are gdn_kernel's bit for bit), stored lane-interleaved -- lane l's
+// q[l], q[l+64], k[l], k[l+64] are consecutive, one 16-byte load in the scan -- and the
+// decay and beta gate of each value head.
+template <int E>
+__global__ __launch_bounds__(256) void gdn_prep_batch_kernel(GdnBatchArgs a) {
+    constexpr int SD = 64 * E;
+    const int lane = threadIdx.x & 63;
+    const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);  // position * key_heads + key head
     const int key_dim = a.key_heads * SD, ch = 2 * key_dim + a.value_heads * SD;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int d = part * (SD / SPLIT) + wave;
-    float* S = a.state + (size_t)h * SD * SD + (size_t)d * SD;
-    float s[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) s[e] = S[lane + 64 * e];
-    const float A = a.ssm_a[h], DT = a.dt[h];
-
-    // inputs of position t: q and k of the key head, v of the row, alpha and beta
-    struct In {
-        float q[E], k[E], v, al, be;
-    };
-    auto load = [&](In& in, int t) {
+    if (pair < a.count * a.key_heads) {
+        const int t = pair / a.key_heads, kh = pair - t * a.key_heads;
         const float* row = a.conv_out + (size_t)t * ch;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            in.q[e] = row[(size_t)kh * SD + lane + 64 * e];
-            in.k[e] = row[key_dim + (size_t)kh * SD + lane + 64 * e];
-        }
-        in.v = row[2 * (size_t)key_dim + (size_t)h * SD + d];
-        in.al = a.alpha[(size_t)t * a.stride + h];
-        in.be = a.beta[(size_t)t * a.stride + h];
-    };
-    In cur, nxt;
-    load(cur, 0);
-    for (int t = 0; t < a.count; ++t) {
-        load(nxt, min(t + 1, a.count - 1));
         // q/k L2 normalisation (backend.cpp:30-35), as gdn_kernel
         float qv[E], kv[E], qs = 0.f, ks = 0.f;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            qv[e] = cur.q[e];
-            kv[e] = cur.k[e];
+            qv[e] = row[(size_t)kh * SD + lane + 64 * e];
+            kv[e] = row[key_dim + (size_t)kh * SD + lane + 64 * e];
             qs += qv[e] * qv[e];
             ks += kv[e] * kv[e];
         }
         qs = wave_sum(qs);
         ks = wave_sum(ks);
         const float qscale = 1.f / sqrtf(qs + a.eps) / sqrtf((float)SD), kscale = 1.f / sqrtf(ks + a.eps);
+        float* dst = a.qk + ((size_t)pair * 64 + lane) * 2 * E;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            qv[e] *= qscale;
-            kv[e] *= kscale;
+            dst[e] = qv[e] * qscale;
+            dst[E + e] = kv[e] * kscale;
         }
-        const float decay = expf(A * softplusf_(cur.al + DT));
-        const float b = sigmoidf_(cur.be);
-        float mem = 0.f;
+    }
+    const int i = blockIdx.x * 256 + threadIdx.x;  // position * value_heads + value head
+    if (i < a.count * a.value_heads) {
+        const int t = i / a.value_heads, h = i - t * a.value_heads;
+        a.gates[2 * (size_t)i] = expf(a.ssm_a[h] * softplusf_(a.alpha[(size_t)t * a.stride + h] + a.dt[h]));
+        a.gates[2 * (size_t)i + 1] = sigmoidf_(a.beta[(size_t)t * a.stride + h]);
+    }
+}
+
+template <int E> __device__ __forceinline__ void load_qk(const float* p, float (&q)[E], float (&k)[E]) {
+    if constexpr (E == 2) {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        q[0] = v.x, q[1] = v.y, k[0] = v.z, k[1] = v.w;
+    } else {
+        const float2 v = *reinterpret_cast<const float2*>(p);
+        q[0] = v.x, k[0] = v.y;
+    }
+}
+
+constexpr int kScanAhead = 8;  // positions whose q/k are in flight ahead of the one in use
+
+// Rows [part*SD/SPLIT, (part+1)*SD/SPLIT) of value head h over all positions; one row
+// per wave, the row's state in registers throughout. The chain per position is the
+// update itself -- two wave reductions -- with the inputs already in registers: q/k of
+// the next kScanAhead positions are in flight, and the row's v, decay and beta gate of
+// 64 positions arrive in one load (lane u holds position t0 + u; the next 64 load while
+// these are used). The raw outputs S.q of 64 positions are collected the same way (lane
+// u) and written with one store.
+template <int E, int SPLIT>
+__global__ __launch_bounds__(kGdnWaves * 64) void gdn_scan_kernel(GdnBatchArgs a) {
+    constexpr int SD = 64 * E, RPW = SD / SPLIT / kGdnWaves, P = kScanAhead;
+    static_assert(RPW == 1, "one row per wave");
+    static_assert(64 % P == 0, "prefetch depth divides the 64-position block");
+    const int h = blockIdx.x / SPLIT, part = blockIdx.x - h * SPLIT, kh = h % a.key_heads;
+    const int key_dim = a.key_heads * SD, ch = 2 * key_dim + a.value_heads * SD;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int d = part * (SD / SPLIT) + wave, last = a.count - 1;
+    float* S = a.state + (size_t)h * SD * SD + (size_t)d * SD;
+    float s[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            s[e] *= decay;
-            mem += s[e] * kv[e];
-        }
-        mem = wave_sum(mem);
-        const float delta = (cur.v - mem) * b;
-        float sum = 0.f;
+    for (int e = 0; e < E; ++e) s[e] = S[lane + 64 * e];
+
+    const size_t qk_step = (size_t)a.key_heads * 64 * 2 * E;  // floats per position
+    const float* qk = a.qk + ((size_t)kh * 64 + lane) * 2 * E;
+    const float* v_col = a.conv_out + 2 * (size_t)key_dim + (size_t)h * SD + d;
+    const size_t o_step = (size_t)a.value_heads * SD;
+    float* o_col = a.o + (size_t)h * SD + d;
+
+    float rq[P][E], rk[P][E];  // position t's q/k sit in slot t % P
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            s[e] += kv[e] * delta;
-            sum += s[e] * qv[e];
+    for (int u = 0; u < P; ++u) load_qk<E>(qk + (size_t)min(u, last) * qk_step, rq[u], rk[u]);
+    auto lane_inputs = [&](int t0, float& v, float& dec, float& b) {
+        const int t = min(t0 + lane, last);
+        v = v_col[(size_t)t * ch];
+        const float2 g = *reinterpret_cast<const float2*>(a.gates + 2 * ((size_t)t * a.value_heads + h));
+        dec = g.x, b = g.y;
+    };
+    // positions t0 .. t0+63 with lane u's v, decay and beta gate of position t0 + u in
+    // (vl, dl, bl), while those of the next 64 load into (vn, dn, bn)
+    auto block = [&](int t0, const float& vl, const float& dl, const float& bl, float& vn, float& dn, float& bn) {
+        lane_inputs(t0 + 64, vn, dn, bn);
+        const int n = min(64, a.count - t0);
+        float ol = 0.f;
+        for (int u0 = 0; u0 < n; u0 += P) {
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                const int u = u0 + j, t = t0 + u;
+                if (u < n) {
+                    const float(&qv)[E] = rq[j];
+                    const float(&kv)[E] = rk[j];
+                    const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vl), u));
+                    const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dl), u));
+                    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bl), u));
+                    float mem = 0.f;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        s[e] *= decay;
+                        mem += s[e] * kv[e];
+                    }
+                    mem = wave_sum(mem);
+                    const float delta = (v - mem) * b;
+                    float sum = 0.f;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        s[e] += kv[e] * delta;
+                        sum += s[e] * qv[e];
+                    }
+                    sum = wave_sum(sum);
+                    ol = lane == u ? sum : ol;
+                }
+                // refill the slot once its position is done, so the load lands in the same
+                // registers (a refill issued while the slot is still read needs a copy at
+                // the loop's back edge, and with it a wait for the load)
+                load_qk<E>(qk + (size_t)min(t + P, last) * qk_step, rq[j], rk[j]);
+            }
         }
-        sum = wave_sum(sum);
-        if (lane == 0) a.o[(size_t)t * a.value_heads * SD + (size_t)h * SD + d] = sum;
-        cur = nxt;
+        if (lane < n) o_col[(size_t)(t0 + lane) * o_step] = ol;
+    };
+    // two register sets in turn, so no copy (and no wait for the next block's loads) sits
+    // between blocks
+    float va, da, ba, vb, db, bb;
+    lane_inputs(0, va, da, ba);
+    // Everything above has arrived before the loop starts, so the wait the compiler
+    // places before each slot's use is the steady state's (the loads of the following
+    // slots stay in flight), not one shaped by the order of these first loads.
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int t0 = 0; t0 < a.count; t0 += 128) {
+        block(t0, va, da, ba, vb, db, bb);
+        if (t0 + 64 < a.count) block(t0 + 64, vb, db, bb, va, da, ba);
     }
 #pragma unroll
     for (int e = 0; e < E; ++e) S[lane + 64 * e] = s[e];
@@ -336,29 +422,43 @@ __global__ __launch_bounds__(64) void gdn_norm_gate_batch_kernel(GdnBatchArgs a)
 }  // namespace
 
 hipError_t launch_gdn_batch(const GdnBatchArgs& a, hipStream_t stream) {
-    if (a.count < 1 || (a.state_dim != 64 && a.state_dim != 128)) return hipErrorInvalidValue;
+    if (a.count < 1 || a.count > 65535 * kConvSpan || (a.state_dim != 64 && a.state_dim != 128))
+        return hipErrorInvalidValue;
     const int ch = 2 * a.key_heads * a.state_dim + a.value_heads * a.state_dim;
-    const dim3 cgrid((ch + 255) / 256), cblock(256);
+    const dim3 cgrid((ch + 255) / 256, (a.count + kConvSpan - 1) / kConvSpan), hgrid((ch + 255) / 256), cblock(256);
+#define EMPRISE_CONV_CASE(W)                                                              \
+    case W:                                                                               \
+        launch_kernel(delta_conv_batch_kernel<W>, cgrid, cblock, 0, stream, a);           \
+        launch_kernel(delta_conv_history_kernel<W>, hgrid, cblock, 0, stream, a);         \
+        break;
     switch (a.conv_width) {
-    case 1: launch_kernel(delta_conv_batch_kernel<1>, cgrid, cblock, 0, stream, a); break;
-    case 2: launch_kernel(delta_conv_batch_kernel<2>, cgrid, cblock, 0, stream, a); break;
-    case 3: launch_kernel(delta_conv_batch_kernel<3>, cgrid, cblock, 0, stream, a); break;
-    case 4: launch_kernel(delta_conv_batch_kernel<4>, cgrid, cblock, 0, stream, a); break;
-    case 5: launch_kernel(delta_conv_batch_kernel<5>, cgrid, cblock, 0, stream, a); break;
-    case 6: launch_kernel(delta_conv_batch_kernel<6>, cgrid, cblock, 0, stream, a); break;
-    case 7: launch_kernel(delta_conv_batch_kernel<7>, cgrid, cblock, 0, stream, a); break;
-    case 8: launch_kernel(delta_conv_batch_kernel<8>, cgrid, cblock, 0, stream, a); break;
+        EMPRISE_CONV_CASE(1)
+        EMPRISE_CONV_CASE(2)
+        EMPRISE_CONV_CASE(3)
+        EMPRISE_CONV_CASE(4)
+        EMPRISE_CONV_CASE(5)
+        EMPRISE_CONV_CASE(6)
+        EMPRISE_CONV_CASE(7)
+        EMPRISE_CONV_CASE(8)
     default: return hipErrorInvalidValue;
     }
+#undef EMPRISE_CONV_CASE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 block(kGdnWaves * 64);
+    const int pgrid = std::max((a.count * a.key_heads + 3) / 4, (a.count * a.value_heads + 255) / 256);
     if (a.state_dim == 64) {
+        launch_kernel(gdn_prep_batch_kernel<1>, dim3(pgrid), dim3(256), 0, stream, a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
         launch_kernel(gdn_scan_kernel<1, 8>, dim3(a.value_heads * 8), block, 0, stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         launch_kernel(gdn_norm_gate_batch_kernel<1>, dim3(a.count * a.value_heads), dim3(64), 0, stream, a);
     } else {
+        launch_kernel(gdn_prep_batch_kernel<2>, dim3(pgrid), dim3(256), 0, stream, a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
         launch_kernel(gdn_scan_kernel<2, 16>, dim3(a.value_heads * 16), block, 0, stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;

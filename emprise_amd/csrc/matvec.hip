@@ -927,6 +927,110 @@ __global__ void dequant_rows_kernel(const uint8_t* w, uint32_t type, int cols, u
         out[i] = decode_element(w, type, cols, row0 + i / cols, (int)(i % cols));
 }
 
+// The same values for the chunked Q6_K / Q4_K layouts, a 4096-column chunk per wave and
+// work item: the streaming matvec's lane loads (lane l holds columns 64l .. 64l+63 of the
+// chunk; the next item's loads are in flight while one is decoded) and the shared element
+// formulas. The decoded chunk passes through LDS so that each store instruction writes 1
+// KiB of consecutive floats (stored from the lanes' own columns, a store would cover 16
+// bytes of each of 64 lines). Lane rows are padded to 17 float4, which keeps both the
+// row-wise writes and the column-wise reads free of bank conflicts.
+constexpr int kDequantGrid = 512;
+
+template <int T> __device__ __forceinline__ void dequant_chunk_values(const SChunk<T, 1>& ch, float4* v) {
+    if constexpr (T == kQ6K) {
+        // unit 4l+j: codes 0..11 are the low 6 bits of plane (t/4)'s word j, codes 12..15
+        // the top 2 bits of the three planes' bytes
+        const float d = half_bits_to_float((uint16_t)ch.d[0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int8_t sc = (int8_t)(ch.sc[0] >> (8 * j));
+            const uint32_t pw[3] = {lane_word(ch.q[0][0], j), lane_word(ch.q[0][1], j), lane_word(ch.q[0][2], j)};
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+                v[4 * j + p] = make_float4(q6k_weight(d, sc, pw[p] & 63), q6k_weight(d, sc, (pw[p] >> 8) & 63),
+                                           q6k_weight(d, sc, (pw[p] >> 16) & 63), q6k_weight(d, sc, (pw[p] >> 24) & 63));
+            float hi[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                hi[b] = q6k_weight(d, sc, (int)(((pw[0] >> (8 * b + 6)) & 3) | (((pw[1] >> (8 * b + 6)) & 3) << 2) |
+                                                (((pw[2] >> (8 * b + 6)) & 3) << 4)));
+            v[4 * j + 3] = make_float4(hi[0], hi[1], hi[2], hi[3]);
+        }
+    } else {
+        // unit 2l+p: codes 0..15 the low nibbles of its 16 bytes, 16..31 the high nibbles
+        const float dd = half_bits_to_float((uint16_t)(ch.dd[0] & 0xffff));
+        const float dm = half_bits_to_float((uint16_t)(ch.dd[0] >> 16));
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t b = (ch.s2[0] >> (8 * p)) & 0xff;
+            const int sc = b & 63, mn = ((b >> 6) << 4) | ((ch.m4[0] >> (4 * p)) & 15);
+#pragma unroll
+            for (int wd = 0; wd < 4; ++wd) {
+                const uint32_t q = lane_word(ch.q[0][p], wd);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    v[8 * p + 4 * h + wd] = make_float4(
+                        q4k_weight(dd, dm, sc, mn, (q >> (4 * h)) & 15), q4k_weight(dd, dm, sc, mn, (q >> (8 + 4 * h)) & 15),
+                        q4k_weight(dd, dm, sc, mn, (q >> (16 + 4 * h)) & 15),
+                        q4k_weight(dd, dm, sc, mn, (q >> (24 + 4 * h)) & 15));
+            }
+        }
+    }
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void dequant_chunks_kernel(const uint8_t* w, int cols, uint64_t row0, uint64_t n,
+                                                             float* out) {
+    __shared__ float4 tile[4][64 * 17];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, chunks = cols / kChunkCols;
+    const uint64_t items = n * (uint64_t)chunks, stride = (uint64_t)gridDim.x * 4;
+    const uint64_t row_bytes = (uint64_t)(cols / 256) * Fmt<T>::block;
+    float4* t = tile[wave];
+    auto load = [&](SChunk<T, 1>& ch, uint64_t item) {
+        const uint64_t r = item / (uint64_t)chunks;
+        const uint8_t* rp = w + (row0 + r) * row_bytes;
+        sload<T, 1>(ch, &rp, (int)(item - r * (uint64_t)chunks), lane);
+    };
+    uint64_t it = (uint64_t)blockIdx.x * 4 + wave;
+    SChunk<T, 1> cur, nxt;
+    if (it < items) load(cur, it);
+    for (; it < items; it += stride) {
+        if (it + stride < items) load(nxt, it + stride);
+        float4 v[16];
+        dequant_chunk_values<T>(cur, v);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t[lane * 17 + i] = v[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // float4 q = 64i + lane of the chunk comes from lane q/16, its float4 q%16; the item
+        // is row r, chunk c, so the chunk starts at r*cols + c*4096 = item*4096
+        float4* o = reinterpret_cast<float4*>(out + it * (uint64_t)kChunkCols);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[64 * i + lane] = t[(4 * i + (lane >> 4)) * 17 + (lane & 15)];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        cur = nxt;
+    }
+}
+
+// The same values for rows whose width is a multiple of 1024 (the GEMM path's weights):
+// workgroup = (row, 1024-column segment) by 32-bit block index, each thread four
+// consecutive columns and one 16-byte store.
+__global__ __launch_bounds__(256) void dequant_rows_1k_kernel(const uint8_t* w, uint32_t type, int cols, uint64_t row0,
+                                                              float* out) {
+    const int segs = cols >> 10;
+    const uint32_t r = blockIdx.x / segs;
+    const int k = (blockIdx.x - r * segs) * 1024 + 4 * threadIdx.x;
+    float4 v;
+    v.x = decode_element(w, type, cols, row0 + r, k);
+    v.y = decode_element(w, type, cols, row0 + r, k + 1);
+    v.z = decode_element(w, type, cols, row0 + r, k + 2);
+    v.w = decode_element(w, type, cols, row0 + r, k + 3);
+    *reinterpret_cast<float4*>(out + (size_t)r * cols + k) = v;
+}
+
 }  // namespace
 
 // ---- host launchers ------------------------------------------------------------------
@@ -975,6 +1079,20 @@ hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, 
 hipError_t launch_dequant_rows(const uint8_t* w, uint32_t type, int cols, uint64_t row0, uint64_t n, float* out,
                                hipStream_t stream) {
     const uint64_t total = n * (uint64_t)cols;
+    const bool aligned = reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    if ((type == kQ6K || type == kQ4K) && cols % kChunkCols == 0 && n > 0 && aligned) {
+        const uint64_t blocks = std::min<uint64_t>((n * (uint64_t)(cols / kChunkCols) + 3) / 4, kDequantGrid);
+        {
+            if (type == kQ6K) launch_kernel(dequant_chunks_kernel<kQ6K>, dim3((unsigned)blocks), dim3(256), 0, stream, w, cols, row0, n, out);
+            else launch_kernel(dequant_chunks_kernel<kQ4K>, dim3((unsigned)blocks), dim3(256), 0, stream, w, cols, row0, n, out);
+            return hipGetLastError();
+        }
+    }
+    if (cols % 1024 == 0 && total > 0 && total / 1024 < (1ull << 31) && reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+        launch_kernel(dequant_rows_1k_kernel, dim3((unsigned)(total / 1024)), dim3(256), 0, stream, w, type, cols, row0,
+                      out);
+        return hipGetLastError();
+    }
     uint64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;

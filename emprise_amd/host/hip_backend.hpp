@@ -5,6 +5,8 @@
 #pragma once
 #include <stdexcept>
 #include <string>
+#include <vector>
+#include <initializer_list>
 
 #include "emprise_hip.h"
 
@@ -75,6 +77,12 @@ public:
     }
     void dev_linear_batch(emprise_weight w, emprise_dev x, uint64_t ldx, emprise_dev y, uint64_t ldy, int k) {
         hip_check(emprise_hip_linear_batch_strided(h_, w, x, ldx, y, ldy, k), "linear_batch");
+    }
+    void dev_linear_batch_many(std::initializer_list<emprise_weight> ws, emprise_dev x, uint64_t ldx, emprise_dev y,
+                               uint64_t ldy, int k) {
+        const std::vector<emprise_weight> w(ws);
+        hip_check(emprise_hip_linear_batch_many(h_, static_cast<int>(w.size()), w.data(), x, ldx, y, ldy, k),
+                  "linear_batch_many");
     }
     void dev_swiglu(emprise_dev gate, emprise_dev up, int n) { hip_check(emprise_hip_swiglu(h_, gate, up, n), "swiglu"); }
     void dev_delta_net(const emprise_hip_delta_net_params& p) { hip_check(emprise_hip_delta_net(h_, &p), "delta_net"); }

@@ -392,7 +392,8 @@ std::vector<float> Model::last_hidden() {
 
 // Positions [0, count) of the prompt at dev_prompt_, in chunks of up to kPrefillChunk
 // tokens: every projection runs once per chunk as a GEMM on the matrix cores (the
-// reference batches 4 positions, model.cpp:355-366; here the whole chunk), the RMSNorms,
+// reference batches 4 positions, model.cpp:355-366; here the whole chunk), the
+// projections of one input stacked into one GEMM (q|k|v; qkv|z|alpha|beta), the RMSNorms,
 // residual adds and SwiGLU run over all rows at once, the GDN conv + state update runs
 // as one scan over the chunk's positions (emprise_hip_delta_net_batch), and attention
 // runs over the chunk at once as FP32 GEMMs with a causal softmax
@@ -424,10 +425,7 @@ void Model::prefill_batched(size_t count) {
             b.dev_rmsnorm_rows(pf_x_, L.attn_norm, pf_xn_, static_cast<int>(H), T, d.eps);
             if (L.recurrent) {
                 const uint64_t W = ch + vd + 2 * vh;
-                b.dev_linear_batch(L.qkv, pf_xn_, H, pf_a_, W, T);
-                b.dev_linear_batch(L.zgate, pf_xn_, H, pf_a_ + ch * 4, W, T);
-                b.dev_linear_batch(L.alpha, pf_xn_, H, pf_a_ + (ch + vd) * 4, W, T);
-                b.dev_linear_batch(L.beta, pf_xn_, H, pf_a_ + (ch + vd + vh) * 4, W, T);
+                b.dev_linear_batch_many({L.qkv, L.zgate, L.alpha, L.beta}, pf_xn_, H, pf_a_, W, T);
                 emprise_hip_delta_net_params p{};
                 p.key_heads = d.key_heads;
                 p.value_heads = d.value_heads;
@@ -449,9 +447,7 @@ void Model::prefill_batched(size_t count) {
                 b.dev_linear_batch(L.out, pf_b_, vd, pf_c_, H, T);
             } else {
                 const uint64_t W = qd + 2 * kvd;
-                b.dev_linear_batch(L.q, pf_xn_, H, pf_a_, W, T);
-                b.dev_linear_batch(L.k, pf_xn_, H, pf_a_ + qd * 4, W, T);
-                b.dev_linear_batch(L.v, pf_xn_, H, pf_a_ + (qd + kvd) * 4, W, T);
+                b.dev_linear_batch_many({L.q, L.k, L.v}, pf_xn_, H, pf_a_, W, T);
                 emprise_hip_attention_params p{};
                 p.heads = d.heads;
                 p.kv_heads = d.kv_heads;

@@ -113,6 +113,12 @@ emprise_status emprise_hip_linear_batch(emprise_hip* h, emprise_weight w, empris
  * reference prefills in chunks of 4 positions, model.cpp:355-366). */
 emprise_status emprise_hip_linear_batch_strided(emprise_hip* h, emprise_weight w, emprise_dev X, uint64_t ldx,
                                                 emprise_dev Y, uint64_t ldy, int K);
+/* linear_batch_strided over n <= 8 weights of one input width, their outputs side by
+ * side: Y[k] = [W_0; W_1; ...] X[k], weight i's rows in the columns that follow weight
+ * i-1's. The stacked rows run as one GEMM (e.g. the q|k|v or recurrent in-projections of
+ * the prefill). Batched prefill support, like linear_batch_strided. */
+emprise_status emprise_hip_linear_batch_many(emprise_hip* h, int n, const emprise_weight* w, emprise_dev X,
+                                             uint64_t ldx, emprise_dev Y, uint64_t ldy, int K);
 
 /* Input transform fused into a projection's prologue. It stands for the reference's
  * dev_add + dev_rmsnorm pair in front of every projection group (model.cpp:429,
@@ -187,7 +193,8 @@ emprise_status emprise_hip_delta_net(emprise_hip* h, const emprise_hip_delta_net
  * model.cpp:355-366): qkv, gate, alpha and beta are the rows of position 0, the rows of
  * position t are `stride` floats further; out receives `count` rows `out_stride` floats
  * apart. Per position the same arithmetic, in the same order, as emprise_hip_delta_net,
- * so outputs and final states equal `count` calls of it. qkv is not modified. */
+ * so outputs and final states equal `count` calls of it. qkv is not modified.
+ * 1 <= count <= 524288. */
 emprise_status emprise_hip_delta_net_batch(emprise_hip* h, const emprise_hip_delta_net_params* p, int count,
                                            uint64_t stride, uint64_t out_stride);
 

@@ -112,8 +112,62 @@ def test_linear_batch_strided(backend, K):
     backend.weight_free(w)
 
 
+@pytest.mark.parametrize("K", [3, 40])
+def test_linear_batch_many(backend, K):
+    """Stacked weights (mixed types) in one batched call: each weight's rows land after
+    the previous weight's, equal to the oracle and bit-equal to one call per weight."""
+    cols, ldy, off = 4096, 700, 11
+    specs = [(Q6_K, 200), (Q4_K, 32), (F32, 16), (Q6_K, 300)]
+    rng = np.random.default_rng(K + 1)
+    raws = [(t, r, matrix(rng, t, r, cols)) for t, r in specs]
+    ws = [backend.upload_weight(t, cols, r, raw) for t, r, raw in raws]
+    X = rng.standard_normal((K, cols)).astype(np.float32)
+    xd = backend.to_device(X)
+    Y0 = np.full((K, ldy), 7.0, np.float32)
+    yd, y1 = backend.to_device(Y0), backend.to_device(Y0)
+    backend.linear_batch_many(ws, xd, cols, yd + off * 4, ldy, K)
+    Y = backend.download(yd, (K, ldy))
+    o = off
+    for (t, r, raw), w in zip(raws, ws):
+        backend.linear_batch_strided(w, xd, cols, y1 + o * 4, ldy, K)
+        for k in range(K):
+            _close(Y[k, o:o + r], oracle.matvec(t, raw, X[k], r))
+        o += r
+    assert np.array_equal(Y, backend.download(y1, (K, ldy)))
+    assert np.all(Y[:, :off] == 7.0) and np.all(Y[:, o:] == 7.0)
+    wn = backend.upload_weight(Q6_K, 2048, 16, matrix(rng, Q6_K, 16, 2048))
+    with pytest.raises(InvalidArgument):  # input widths differ
+        backend.linear_batch_many([ws[0], wn], xd, cols, yd, ldy, K)
+    for b in (xd, yd, y1):
+        backend.free(b)
+    for w in ws + [wn]:
+        backend.weight_free(w)
+
+
+def test_linear_batch_many_over_scratch_blocks(backend):
+    """Stacked rows beyond one dequantisation block (16384 rows of 4096): the second
+    weight straddles the block boundary; bit-equal to one call per weight."""
+    cols, K = 4096, 8
+    rng = np.random.default_rng(5)
+    specs = [(Q6_K, 12000), (Q4_K, 6000)]
+    ws = [backend.upload_weight(t, cols, r, matrix(rng, t, r, cols)) for t, r in specs]
+    ldy = sum(r for _, r in specs)
+    xd = backend.to_device(rng.standard_normal((K, cols)).astype(np.float32))
+    yd, y1 = backend.alloc(K * ldy * 4), backend.alloc(K * ldy * 4)
+    backend.linear_batch_many(ws, xd, cols, yd, ldy, K)
+    backend.linear_batch_strided(ws[0], xd, cols, y1, ldy, K)
+    backend.linear_batch_strided(ws[1], xd, cols, y1 + specs[0][1] * 4, ldy, K)
+    assert np.array_equal(backend.download(yd, (K, ldy)), backend.download(y1, (K, ldy)))
+    for b in (xd, yd, y1):
+        backend.free(b)
+    for w in ws:
+        backend.weight_free(w)
+
+
+# widths: chunked layout (one and two 4096-column chunks), multiples of 1024, others
 @pytest.mark.parametrize("wtype,rows,cols", [(Q6_K, 300, 4096), (Q4_K, 300, 4096), (Q6_K, 5, 1536), (Q4_K, 7, 512),
-                                             (F16, 9, 512), (BF16, 9, 512), (F32, 9, 256)])
+                                             (Q6_K, 3, 8192), (Q4_K, 5, 8192), (Q6_K, 6, 2048), (Q4_K, 6, 3072),
+                                             (F16, 9, 512), (BF16, 9, 512), (F32, 9, 256), (F32, 4, 1024)])
 def test_dequantize_bit_exact(backend, wtype, rows, cols):
     rng = np.random.default_rng(11)
     raw = matrix(rng, wtype, rows, cols)
@@ -123,6 +177,11 @@ def test_dequantize_bit_exact(backend, wtype, rows, cols):
     got = backend.download(out, rows * cols)
     ref = oracle.dequantize(wtype, raw, rows * cols)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # a block of rows starting past row 0 (the GEMM path dequantises in blocks)
+    r0, n = rows // 3, rows - rows // 3 - 1
+    backend.dequantize_rows(w, r0, n, out)
+    got = backend.download(out, n * cols)
+    assert np.array_equal(got.view(np.uint32), ref[r0 * cols:(r0 + n) * cols].view(np.uint32))
     # the device re-layout is lossless: reading it back restores the GGUF bytes
     assert backend.weight_download_gguf(w, len(raw)) == raw
     backend.free(out)

@@ -153,8 +153,11 @@ def test_delta_net_steps(backend, kh, vh, sd, cw):
         assert np.array_equal(backend.download(conv_g, ch * cw), conv_c)  # conv history is a copy
 
 
+# counts: one position; fewer than conv_width - 1; within one 64-position block of the
+# scan; over three blocks (both register sets of the scan, a partial last block)
 @pytest.mark.parametrize("kh,vh,sd,cw,count", [(16, 32, 128, 4, 37), (4, 8, 64, 4, 9), (4, 8, 64, 3, 1),
-                                               (16, 32, 128, 4, 1)])
+                                               (16, 32, 128, 4, 1), (4, 8, 64, 4, 2), (16, 32, 128, 4, 150),
+                                               (4, 8, 64, 2, 130)])
 def test_delta_net_batch_matches_steps(backend, kh, vh, sd, cw, count):
     """emprise_hip_delta_net_batch (the prefill scan over `count` positions, rows in a
     strided [qkv | gate | alpha | beta] layout) equals `count` calls of delta_net: every
@@ -214,7 +217,7 @@ def test_delta_net_batch_rejects_bad_strides(backend):
     buf = backend.alloc(4 * (ch + vd + 2 * vh))
     st = backend.alloc(4 * (ch * cw + vh * sd * sd))
     p = DeltaNetParams(kh, vh, sd, cw, 1e-6, buf, buf, buf, buf, wconv, wa, wdt, wn, st, st, buf)
-    for count, stride, out_stride in ((0, ch, vd), (2, ch - 1, vd), (2, ch, vd - 1)):
+    for count, stride, out_stride in ((0, ch, vd), (2, ch - 1, vd), (2, ch, vd - 1), ((1 << 19) + 1, ch, vd)):
         with pytest.raises(InvalidArgument):
             backend.delta_net_batch(p, count, stride, out_stride)
 
