@@ -461,20 +461,20 @@ hipError_t launch_attention_batch(const AttnBatchArgs& a, hipStream_t stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int kvd = a.kv_heads * hd;
-    for (int h = 0; h < a.heads; ++h) {  // S_h = Q_h K_kvh^T
-        e = launch_gemm_f32(a.q + (size_t)h * hd, a.keys + (size_t)(h / group) * hd, a.scores + (size_t)h * a.count * a.lp,
-                            a.count, L, hd, a.heads * hd, kvd, a.lp, stream);
-        if (e != hipSuccess) return e;
-    }
+    // S_h = Q_h K_kvh^T for every head in one launch; tiles wholly past the causal limit
+    // are skipped (the softmax reads keys 0 .. first+t of row t only)
+    e = launch_gemm_f32_heads(a.q, a.keys, a.scores, a.count, L, hd, a.heads * hd, kvd, a.lp, a.heads, group,
+                              (size_t)hd, (size_t)hd, (size_t)a.count * a.lp, true, false, a.first, stream);
+    if (e != hipSuccess) return e;
     launch_kernel(attn_softmax_batch_kernel, dim3(a.heads * a.count), dim3(256), 0, stream, a);
     launch_kernel(attn_vt_batch_kernel, dim3(a.lp / 32, hd / 32, a.kv_heads), dim3(256), 0, stream, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    for (int h = 0; h < a.heads; ++h) {  // O_h = P_h V_kvh
-        e = launch_gemm_f32(a.scores + (size_t)h * a.count * a.lp, a.vt + (size_t)(h / group) * hd * a.lp,
-                            a.o + (size_t)h * hd, a.count, hd, a.lp, a.lp, a.lp, a.heads * hd, stream);
-        if (e != hipSuccess) return e;
-    }
+    // O_h = P_h V_kvh for every head in one launch, each tile's K loop ending at its rows'
+    // last key (P is zero past it)
+    e = launch_gemm_f32_heads(a.scores, a.vt, a.o, a.count, hd, a.lp, a.lp, a.lp, a.heads * hd, a.heads, group,
+                              (size_t)a.count * a.lp, (size_t)hd * a.lp, (size_t)hd, false, true, a.first, stream);
+    if (e != hipSuccess) return e;
     const size_t n = (size_t)a.count * a.heads * hd;
     launch_kernel(attn_gate_batch_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a);
     return hipGetLastError();

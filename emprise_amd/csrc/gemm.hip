@@ -28,13 +28,26 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int GM = 128, GN = 128, GK = 16, GPAD = 4;
 
+// Batch z of a launch (blockIdx.z) multiplies A + z*sA by B + (z/bdiv)*sB into C + z*sC
+// (the heads of attention, bdiv q heads per kv head). Causal forms, for the attention of
+// a chunk whose row m may use keys 0 .. first+m: kCausalKeysN skips the tiles whose keys
+// (N) all lie past every row of the tile; kCausalKeysK stops the K loop of a tile after
+// the last key any of its rows may use (A is zero beyond it).
+enum { kCausalNone = 0, kCausalKeysN = 1, kCausalKeysK = 2 };
+
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int M, int N, int K, int lda, int ldb,
-                                                      int ldc) {
+                                                      int ldc, size_t sA, size_t sB, size_t sC, int bdiv, int causal,
+                                                      int first) {
     __shared__ __align__(16) float As[2][GK][GM + GPAD];
     __shared__ __align__(16) float Bs[2][GK][GN + GPAD];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN;
+    if (causal == kCausalKeysN && n0 >= first + m0 + GM) return;  // whole workgroup, before any barrier
+    if (causal == kCausalKeysK) K = min(K, (first + m0 + GM + GK - 1) / GK * GK);
+    A += blockIdx.z * sA;
+    B += (blockIdx.z / bdiv) * sB;
+    C += blockIdx.z * sC;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
 
     // global -> register staging of one 128 x 16 slice of A and of B: thread t loads
@@ -117,7 +130,21 @@ hipError_t launch_gemm_f32(const float* A, const float* B, float* C, int M, int 
                            hipStream_t stream) {
     if (M < 1 || N < 1 || K < GK || K % GK || lda % 4 || ldb % 4) return hipErrorInvalidValue;
     const dim3 grid((N + GN - 1) / GN, (M + GM - 1) / GM);
-    launch_kernel(gemm_f32_kernel, grid, dim3(256), 0, stream, A, B, C, M, N, K, lda, ldb, ldc);
+    launch_kernel(gemm_f32_kernel, grid, dim3(256), 0, stream, A, B, C, M, N, K, lda, ldb, ldc, (size_t)0, (size_t)0,
+                  (size_t)0, 1, (int)kCausalNone, 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_f32_heads(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb,
+                                 int ldc, int batch, int bdiv, size_t sA, size_t sB, size_t sC, bool causal_keys_n,
+                                 bool causal_keys_k, int first, hipStream_t stream) {
+    if (M < 1 || N < 1 || K < GK || K % GK || lda % 4 || ldb % 4 || batch < 1 || batch > 65535 || bdiv < 1 ||
+        (causal_keys_n && causal_keys_k) || first < 0 || sA % 4 || sB % 4)
+        return hipErrorInvalidValue;
+    const dim3 grid((N + GN - 1) / GN, (M + GM - 1) / GM, batch);
+    const int causal = causal_keys_n ? kCausalKeysN : causal_keys_k ? kCausalKeysK : kCausalNone;
+    launch_kernel(gemm_f32_kernel, grid, dim3(256), 0, stream, A, B, C, M, N, K, lda, ldb, ldc, sA, sB, sC, bdiv,
+                  causal, first);
     return hipGetLastError();
 }
 

@@ -84,6 +84,14 @@ hipError_t launch_dequant_rows(const uint8_t* w, uint32_t type, int cols, uint64
 // K must be a multiple of 16; lda and ldb multiples of 4 (16-byte rows).
 hipError_t launch_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
                            hipStream_t stream);
+// `batch` products in one launch (grid z): C + z*sC = (A + z*sA) (B + (z/bdiv)*sB)^T.
+// causal_keys_n: N indexes keys and row m of a chunk uses keys <= first + m, so tiles
+// past every row's last key are skipped (their C is left unwritten); causal_keys_k: the
+// same with K indexing keys, each tile's K loop ending after its rows' last key (A must
+// be zero beyond it).
+hipError_t launch_gemm_f32_heads(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb,
+                                 int ldc, int batch, int bdiv, size_t sA, size_t sB, size_t sC, bool causal_keys_n,
+                                 bool causal_keys_k, int first, hipStream_t stream);
 
 // ---- Gated DeltaNet ----
 struct GdnArgs {
