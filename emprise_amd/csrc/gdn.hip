@@ -302,49 +302,63 @@ template <int E> __device__ __forceinline__ void load_qk(const float* p, float (
 }
 
 constexpr int kScanAhead = 8;  // positions whose q/k are in flight ahead of the one in use
+// workgroups per value head of the scan at state_dim 64 / 128: one row per wave (two
+// rows per wave measured the same, 15.9 ms per 2048-token 9B prefill: the chain of wave
+// reductions bounds it, not the loads)
+constexpr int kScanSplit1 = 8, kScanSplit2 = 16;
 
-// Rows [part*SD/SPLIT, (part+1)*SD/SPLIT) of value head h over all positions; one row
-// per wave, the row's state in registers throughout. The chain per position is the
-// update itself -- two wave reductions -- with the inputs already in registers: q/k of
-// the next kScanAhead positions are in flight, and the row's v, decay and beta gate of
-// 64 positions arrive in one load (lane u holds position t0 + u; the next 64 load while
+// Rows [part*SD/SPLIT, (part+1)*SD/SPLIT) of value head h over all positions; RPW
+// consecutive rows per wave, their states in registers throughout. The chain per
+// position is the update itself -- two wave reductions per row, the rows' chains
+// interleaved -- with the inputs already in registers: q/k of the next kScanAhead
+// positions are in flight, and each row's v and the head's decay and beta gate of 64
+// positions arrive in one load each (lane u holds position t0 + u; the next 64 load while
 // these are used). The raw outputs S.q of 64 positions are collected the same way (lane
-// u) and written with one store.
+// u) and written with one store per row.
 template <int E, int SPLIT>
 __global__ __launch_bounds__(kGdnWaves * 64) void gdn_scan_kernel(GdnBatchArgs a) {
     constexpr int SD = 64 * E, RPW = SD / SPLIT / kGdnWaves, P = kScanAhead;
-    static_assert(RPW == 1, "one row per wave");
+    static_assert(RPW >= 1 && RPW <= 4, "rows per wave");
     static_assert(64 % P == 0, "prefetch depth divides the 64-position block");
     const int h = blockIdx.x / SPLIT, part = blockIdx.x - h * SPLIT, kh = h % a.key_heads;
     const int key_dim = a.key_heads * SD, ch = 2 * key_dim + a.value_heads * SD;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int d = part * (SD / SPLIT) + wave, last = a.count - 1;
-    float* S = a.state + (size_t)h * SD * SD + (size_t)d * SD;
-    float s[E];
+    const int d0 = part * (SD / SPLIT) + wave * RPW, last = a.count - 1;
+    float* S = a.state + (size_t)h * SD * SD + (size_t)d0 * SD;
+    float s[RPW][E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) s[e] = S[lane + 64 * e];
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int e = 0; e < E; ++e) s[r][e] = S[(size_t)r * SD + lane + 64 * e];
 
     const size_t qk_step = (size_t)a.key_heads * 64 * 2 * E;  // floats per position
     const float* qk = a.qk + ((size_t)kh * 64 + lane) * 2 * E;
-    const float* v_col = a.conv_out + 2 * (size_t)key_dim + (size_t)h * SD + d;
+    const float* v_col = a.conv_out + 2 * (size_t)key_dim + (size_t)h * SD + d0;
     const size_t o_step = (size_t)a.value_heads * SD;
-    float* o_col = a.o + (size_t)h * SD + d;
+    float* o_col = a.o + (size_t)h * SD + d0;
 
     float rq[P][E], rk[P][E];  // position t's q/k sit in slot t % P
 #pragma unroll
     for (int u = 0; u < P; ++u) load_qk<E>(qk + (size_t)min(u, last) * qk_step, rq[u], rk[u]);
-    auto lane_inputs = [&](int t0, float& v, float& dec, float& b) {
-        const int t = min(t0 + lane, last);
-        v = v_col[(size_t)t * ch];
-        const float2 g = *reinterpret_cast<const float2*>(a.gates + 2 * ((size_t)t * a.value_heads + h));
-        dec = g.x, b = g.y;
+    // lane u: the rows' v and the head's decay and beta gate of position t0 + u
+    struct Lanes {
+        float v[RPW], dec, b;
     };
-    // positions t0 .. t0+63 with lane u's v, decay and beta gate of position t0 + u in
-    // (vl, dl, bl), while those of the next 64 load into (vn, dn, bn)
-    auto block = [&](int t0, const float& vl, const float& dl, const float& bl, float& vn, float& dn, float& bn) {
-        lane_inputs(t0 + 64, vn, dn, bn);
+    auto lane_inputs = [&](int t0, Lanes& l) {
+        const int t = min(t0 + lane, last);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) l.v[r] = v_col[(size_t)t * ch + r];
+        const float2 g = *reinterpret_cast<const float2*>(a.gates + 2 * ((size_t)t * a.value_heads + h));
+        l.dec = g.x, l.b = g.y;
+    };
+    // positions t0 .. t0+63 with their lane inputs in `cur`, while those of the next 64
+    // load into `nxt`
+    auto block = [&](int t0, const Lanes& cur, Lanes& nxt) {
+        lane_inputs(t0 + 64, nxt);
         const int n = min(64, a.count - t0);
-        float ol = 0.f;
+        float ol[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) ol[r] = 0.f;
         for (int u0 = 0; u0 < n; u0 += P) {
 #pragma unroll
             for (int j = 0; j < P; ++j) {
@@ -352,25 +366,36 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_scan_kernel(GdnBatchArgs a
                 if (u < n) {
                     const float(&qv)[E] = rq[j];
                     const float(&kv)[E] = rk[j];
-                    const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vl), u));
-                    const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dl), u));
-                    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bl), u));
-                    float mem = 0.f;
+                    const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.dec), u));
+                    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.b), u));
+                    float mem[RPW], sum[RPW];
 #pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        s[e] *= decay;
-                        mem += s[e] * kv[e];
-                    }
-                    mem = wave_sum(mem);
-                    const float delta = (v - mem) * b;
-                    float sum = 0.f;
+                    for (int r = 0; r < RPW; ++r) {
+                        mem[r] = 0.f;
 #pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        s[e] += kv[e] * delta;
-                        sum += s[e] * qv[e];
+                        for (int e = 0; e < E; ++e) {
+                            s[r][e] *= decay;
+                            mem[r] += s[r][e] * kv[e];
+                        }
                     }
-                    sum = wave_sum(sum);
-                    ol = lane == u ? sum : ol;
+#pragma unroll
+                    for (int r = 0; r < RPW; ++r) mem[r] = wave_sum(mem[r]);
+#pragma unroll
+                    for (int r = 0; r < RPW; ++r) {
+                        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.v[r]), u));
+                        const float delta = (v - mem[r]) * b;
+                        sum[r] = 0.f;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) {
+                            s[r][e] += kv[e] * delta;
+                            sum[r] += s[r][e] * qv[e];
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < RPW; ++r) {
+                        sum[r] = wave_sum(sum[r]);
+                        ol[r] = lane == u ? sum[r] : ol[r];
+                    }
                 }
                 // refill the slot once its position is done, so the load lands in the same
                 // registers (a refill issued while the slot is still read needs a copy at
@@ -378,22 +403,26 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_scan_kernel(GdnBatchArgs a
                 load_qk<E>(qk + (size_t)min(t + P, last) * qk_step, rq[j], rk[j]);
             }
         }
-        if (lane < n) o_col[(size_t)(t0 + lane) * o_step] = ol;
+        if (lane < n)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) o_col[(size_t)(t0 + lane) * o_step + r] = ol[r];
     };
     // two register sets in turn, so no copy (and no wait for the next block's loads) sits
     // between blocks
-    float va, da, ba, vb, db, bb;
-    lane_inputs(0, va, da, ba);
+    Lanes la, lb;
+    lane_inputs(0, la);
     // Everything above has arrived before the loop starts, so the wait the compiler
     // places before each slot's use is the steady state's (the loads of the following
     // slots stay in flight), not one shaped by the order of these first loads.
     __builtin_amdgcn_s_waitcnt(0);
     for (int t0 = 0; t0 < a.count; t0 += 128) {
-        block(t0, va, da, ba, vb, db, bb);
-        if (t0 + 64 < a.count) block(t0 + 64, vb, db, bb, va, da, ba);
+        block(t0, la, lb);
+        if (t0 + 64 < a.count) block(t0 + 64, lb, la);
     }
 #pragma unroll
-    for (int e = 0; e < E; ++e) S[lane + 64 * e] = s[e];
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int e = 0; e < E; ++e) S[(size_t)r * SD + lane + 64 * e] = s[r][e];
 }
 
 // Per-head RMSNorm with ssm_norm, then SiLU(gate) (backend.cpp:57-58), as gdn_kernel's
@@ -451,7 +480,7 @@ hipError_t launch_gdn_batch(const GdnBatchArgs& a, hipStream_t stream) {
         launch_kernel(gdn_prep_batch_kernel<1>, dim3(pgrid), dim3(256), 0, stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
-        launch_kernel(gdn_scan_kernel<1, 8>, dim3(a.value_heads * 8), block, 0, stream, a);
+        launch_kernel(gdn_scan_kernel<1, kScanSplit1>, dim3(a.value_heads * kScanSplit1), block, 0, stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         launch_kernel(gdn_norm_gate_batch_kernel<1>, dim3(a.count * a.value_heads), dim3(64), 0, stream, a);
@@ -459,7 +488,7 @@ hipError_t launch_gdn_batch(const GdnBatchArgs& a, hipStream_t stream) {
         launch_kernel(gdn_prep_batch_kernel<2>, dim3(pgrid), dim3(256), 0, stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
-        launch_kernel(gdn_scan_kernel<2, 16>, dim3(a.value_heads * 16), block, 0, stream, a);
+        launch_kernel(gdn_scan_kernel<2, kScanSplit2>, dim3(a.value_heads * kScanSplit2), block, 0, stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         launch_kernel(gdn_norm_gate_batch_kernel<2>, dim3(a.count * a.value_heads), dim3(64), 0, stream, a);

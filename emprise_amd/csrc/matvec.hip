@@ -644,11 +644,7 @@ __global__ __launch_bounds__(W * 64) void matvec_stream_kernel(MvArgs a) {
             const int cw = a.conv_width, r = lane / cw, j = lane - r * cw, row = it.row0 + r;
             const bool on = valid && it.seg == 0 && r < R && row < a.seg[0].rows;
             const size_t o = on ? (size_t)row * cw + j : 0;
-            // global-address-space loads: through a generic pointer these would be flat
-            // loads, which also count against lgkmcnt, and the row epilogue's shuffles
-            // would then wait for the next item's loads
-            const float h = *(const EMPRISE_GLOBAL float*)(on ? a.conv_state + o : a.x);
-            const float k = *(const EMPRISE_GLOBAL float*)(on ? a.conv_w + o : a.x);
+            const float h = *(on ? a.conv_state + o : a.x), k = *(on ? a.conv_w + o : a.x);
             it.conv_h = on ? h : 0.f;
             it.conv_k = on ? k : 0.f;
         }
@@ -693,10 +689,11 @@ __global__ __launch_bounds__(W * 64) void matvec_stream_kernel(MvArgs a) {
 #pragma unroll
     for (int r = 0; r < NA; ++r) acc[r] = 0.f;
 
-    // The row epilogue of item `it` (already computed into acc) after a row group's last
-    // chunk. It runs after the refill of the item's buffer has been issued: its
-    // reductions, shuffles and stores would otherwise hold back the next weight loads.
-    auto epilogue = [&](const SItem<NA>& it) {
+    // Computes the item held in `buf`, runs the row epilogue after a row group's last
+    // chunk, then refills `buf` with the item D ahead (the other buffers hold the next).
+    auto finish = [&](SChunk<T, NA>& buf, SItem<NA>& it) {
+        if constexpr (Q8) scompute_q8<NA>(buf, acc, xq, xscale, qsum, it.c, lane);
+        else scompute<T, NA>(buf, acc, xs, usum, it.c, lane);
         if (it.c == cpr - 1) {
 #pragma unroll
             for (int r = 0; r < NA; ++r) acc[r] = wave_sum(acc[r]);
@@ -748,29 +745,15 @@ __global__ __launch_bounds__(W * 64) void matvec_stream_kernel(MvArgs a) {
             for (int r = 0; r < NA; ++r) acc[r] = 0.f;
         }
     };
-    // items are visited in sequence order, so once one is past the end so are the rest.
-    // Per item: compute from its buffer, refill the buffer with the item D ahead (the
-    // other buffers hold the next), then the finished item's row epilogue (for the conv
-    // variant, the epilogue before the refill).
+    // items are visited in sequence order, so once one is past the end so are the rest
     bool live = its[0].g < a.groups;
     while (live) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             if (live) {
-                if constexpr (Q8) scompute_q8<NA>(bufs[k], acc, xq, xscale, qsum, its[k].c, lane);
-                else scompute<T, NA>(bufs[k], acc, xs, usum, its[k].c, lane);
-                if constexpr (CONV) {
-                    // measured: the conv epilogue (history shuffles and stores) is
-                    // faster ahead of the refill (12.1 against 12.7 us per in-projection)
-                    epilogue(its[k]);
-                    skip(its[k], D);
-                    iload(bufs[k], its[k]);
-                } else {
-                    const SItem<NA> done = its[k];
-                    skip(its[k], D);
-                    iload(bufs[k], its[k]);
-                    epilogue(done);
-                }
+                finish(bufs[k], its[k]);
+                skip(its[k], D);
+                iload(bufs[k], its[k]);
                 live = its[(k + 1) % D].g < a.groups;
             }
         }
