@@ -381,7 +381,10 @@ def main():
                 "9b_q4km": "9B-shape qwen35 Q4_K_M-mix greedy decode, batch 1",
                 "tiny": "tiny qwen35 Q6_K greedy decode, batch 1"}[args.model]
     line = {
-        "metric": "decode tok/s, 9B-shape Q6_K batch 1, 1xMI355X; % of HBM roofline",
+        # the headline metric, worded exactly as quoted; other models name their weights
+        "metric": {"9b_q6k": "decode tok/s, 9B-shape Q6_K batch 1, 1×MI355X; % of HBM roofline",
+                   "9b_q4km": "decode tok/s, 9B-shape Q4_K_M-mix batch 1, 1×MI355X; % of HBM roofline",
+                   "tiny": "decode tok/s, tiny qwen35 Q6_K batch 1, 1×MI355X"}[args.model],
         "value": round(value, 2),
         "unit": "tok/s",
         "n_gpus": 1,
