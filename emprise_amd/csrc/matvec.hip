@@ -488,7 +488,8 @@ __device__ __forceinline__ void sinput_issue(const MvArgs& a, SInput<SB, DN>& s)
 // x_out), RMSNorm, the LDS store (chunk_slot order; natural order for Q8) and the
 // per-unit input sums, reduced across the UNIT/4 consecutive threads that hold a unit.
 template <int UNIT, bool Q8, int SB, bool DN>
-__device__ __forceinline__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, float* usum, float* red) {
+__device__ __forceinline__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s, float* xs, float* usum, float* red,
+                                              int8_t* xq, float* xscale, int* qsum) {
     const int n4 = a.cols / 4;
     const bool writer = a.x_out && blockIdx.x == 0;
     float4* xs4 = reinterpret_cast<float4*>(xs);
@@ -540,9 +541,37 @@ __device__ __forceinline__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s
     for (int k = 0; k < SB; ++k) {
         const int i = threadIdx.x + k * blockDim.x;
         if constexpr (Q8) {
-            // stored by component: a whole-float4 copy under this predicate was lowered
-            // through scratch memory
-            if (i < n4) xs4[i] = make_float4(s.x[k].x, s.x[k].y, s.x[k].z, s.x[k].w);
+            // quantised straight from registers, sstage_q8's rule and layout: a 32-value
+            // block is the float4 of 8 consecutive threads (amax over them), a 16-value
+            // unit those of 4 (its code sum), 4 codes per thread in one 32-bit store
+            const float4 v = s.x[k];
+            float amax = 0.f;
+            amax = fmaxf(amax, fabsf(v.x));
+            amax = fmaxf(amax, fabsf(v.y));
+            amax = fmaxf(amax, fabsf(v.z));
+            amax = fmaxf(amax, fabsf(v.w));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+            const float sc = amax / 127.f;
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            int part = 0;
+            uint32_t packed = 0;
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) {
+                const int q = sc != 0.f ? (int)roundf(vv[c4] / sc) : 0;
+                part += q;
+                packed |= (uint32_t)(q & 0xff) << (8 * c4);
+            }
+            part += __shfl_xor(part, 1, 64);
+            part += __shfl_xor(part, 2, 64);
+            if (i < n4) {
+                const int e = i >> 1, u = i >> 2, c = u >> 8, w = u & 255;
+                reinterpret_cast<uint32_t*>(xq)[(((((c * 4 + (w & 3)) * 64 + (w >> 2)) << 1) + (e & 1)) << 1) + (i & 1)] =
+                    packed;
+                if ((i & 3) == 0) qsum[u] = part;
+                if ((i & 7) == 0) xscale[i >> 3] = half_bits_to_float(float_to_half_bits(sc));
+            }
         } else {
             if (i < n4) xs4[chunk_slot(i)] = s.x[k];
             float t = (s.x[k].x + s.x[k].y) + (s.x[k].z + s.x[k].w);
@@ -675,9 +704,9 @@ __global__ __launch_bounds__(W * 64) void matvec_stream_kernel(MvArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    if constexpr (SM != 0) sinput_finish<UW, Q8, SB, DN>(a, sin, xs, usum, red);
+    if constexpr (SM != 0) sinput_finish<UW, Q8, SB, DN>(a, sin, xs, usum, red, xq, xscale, qsum);
     else sstage<UW, Q8>(a, xs, usum, red);
-    if constexpr (Q8) {
+    if constexpr (Q8 && SM == 0) {
         __syncthreads();
         sstage_q8(a.cols, xs, xq, xscale, qsum);
     }
