@@ -443,6 +443,8 @@ def host_lib() -> ctypes.CDLL:
     lib.emprise_model_evaluate.argtypes = [vp, ctypes.c_int, P(ctypes.c_float)]
     lib.emprise_model_last_hidden.restype = ctypes.c_int
     lib.emprise_model_last_hidden.argtypes = [vp, P(ctypes.c_float)]
+    lib.emprise_model_prefill.restype = ctypes.c_int
+    lib.emprise_model_prefill.argtypes = [vp, P(ctypes.c_int), ctypes.c_size_t, P(ctypes.c_float)]
     lib.emprise_model_generate.restype = ctypes.c_int
     lib.emprise_model_generate.argtypes = [vp, P(ctypes.c_int), ctypes.c_size_t, ctypes.c_size_t, P(ctypes.c_int),
                                            P(ctypes.c_size_t), P(ctypes.c_double)]
@@ -522,6 +524,15 @@ class Model:
         out = np.empty(self.info.vocab, dtype=np.float32) if logits else None
         ptr = out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if logits else None
         _host_check(host_lib().emprise_model_evaluate(self.m, token, ptr))
+        return out
+
+    def prefill(self, tokens, logits: bool = True):
+        """Model::prefill: tokens from the current position on (batched), the last
+        position's logits."""
+        p = (ctypes.c_int * len(tokens))(*tokens)
+        out = np.empty(self.info.vocab, dtype=np.float32) if logits else None
+        ptr = out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if logits else None
+        _host_check(host_lib().emprise_model_prefill(self.m, p, len(tokens), ptr))
         return out
 
     def last_hidden(self) -> np.ndarray:

@@ -104,6 +104,17 @@ emprise_status emprise_model_evaluate(emprise_model* m, int token, float* logits
     });
 }
 
+emprise_status emprise_model_prefill(emprise_model* m, const int* tokens, size_t n, float* logits) {
+    if (!m || (!tokens && n)) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] {
+        auto v = m->model->prefill(std::vector<int>(tokens, tokens + n), logits != nullptr);
+        if (logits) std::memcpy(logits, v.data(), v.size() * sizeof(float));
+    });
+}
+
 emprise_status emprise_model_last_hidden(emprise_model* m, float* hidden) {
     if (!m || !hidden) {
         g_error = "null argument";

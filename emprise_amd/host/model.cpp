@@ -390,7 +390,8 @@ std::vector<float> Model::last_hidden() {
     return h;
 }
 
-// Positions [0, count) of the prompt at dev_prompt_, in chunks of up to kPrefillChunk
+// Positions [start, start + count) of the tokens at dev_prompt_ (token of position p at
+// index p), in chunks of up to kPrefillChunk
 // tokens: every projection runs once per chunk as a GEMM on the matrix cores (the
 // reference batches 4 positions, model.cpp:355-366; here the whole chunk), the
 // projections of one input stacked into one GEMM (q|k|v; qkv|z|alpha|beta), the RMSNorms,
@@ -398,7 +399,7 @@ std::vector<float> Model::last_hidden() {
 // as one scan over the chunk's positions (emprise_hip_delta_net_batch), and attention
 // runs over the chunk at once as FP32 GEMMs with a causal softmax
 // (emprise_hip_attention_batch). Op order is that of the unfused decode step.
-void Model::prefill_batched(size_t count) {
+void Model::prefill_batched(size_t start, size_t count) {
     constexpr size_t kPrefillChunk = 2048;
     HipBackend& b = *backend_;
     const emprise_model_info& d = info_;
@@ -420,7 +421,7 @@ void Model::prefill_batched(size_t count) {
     }
     for (size_t p0 = 0; p0 < count; p0 += rows) {
         const int T = static_cast<int>(std::min(rows, count - p0));
-        b.dev_embed_rows(embd_, dev_prompt_ + p0 * sizeof(int), T, pf_x_);
+        b.dev_embed_rows(embd_, dev_prompt_ + (start + p0) * sizeof(int), T, pf_x_);
         for (const Layer& L : layers_) {
             b.dev_rmsnorm_rows(pf_x_, L.attn_norm, pf_xn_, static_cast<int>(H), T, d.eps);
             if (L.recurrent) {
@@ -460,7 +461,7 @@ void Model::prefill_batched(size_t count) {
                 p.k_norm = L.k_norm;
                 p.keys = L.keys;
                 p.values = L.values;
-                b.dev_attention_batch(p, pf_a_, T, W, static_cast<int>(p0), pf_b_, ao);
+                b.dev_attention_batch(p, pf_a_, T, W, static_cast<int>(start + p0), pf_b_, ao);
                 b.dev_linear_batch(L.o, pf_b_, ao, pf_c_, H, T);
             }
             b.dev_add(pf_x_, pf_c_, static_cast<int>(T * H));
@@ -487,7 +488,7 @@ std::vector<int> Model::generate(const std::vector<int>& prompt, size_t count, s
     backend_->event(0);
     // prefill: every prompt position but the last skips the output head
     if (opt_.batch_prefill_min && static_cast<size_t>(n - 1) >= opt_.batch_prefill_min) {
-        prefill_batched(static_cast<size_t>(n - 1));
+        prefill_batched(0, static_cast<size_t>(n - 1));
         set_state(n - 1, prompt[static_cast<size_t>(n - 1)], n);
     } else {
         set_state(0, prompt[0], n);
@@ -514,8 +515,53 @@ std::vector<int> Model::generate(const std::vector<int>& prompt, size_t count, s
         out.push_back(hist[i]);
         if (arrivals) arrivals->push_back(backend_->elapsed(0, static_cast<int>(1 + i)) * 1e-3);
     }
-    position_ = static_cast<size_t>(n) + count;
+    // The reference evaluates the prompt and every emitted token but the last
+    // (model.cpp:497-502): n + count - 1 positions, and fewer when EOS stops it. The
+    // device ran all count steps (the count-th only picked the last token), so without
+    // EOS its state is the reference's. After EOS it has moved past the reference's
+    // stopping point; the state is rebuilt by evaluating the prompt and the emitted
+    // tokens again (n + emitted positions, as the reference leaves it).
+    if (out.size() == count) {
+        position_ = static_cast<size_t>(n) + count - 1;
+    } else {
+        std::vector<int> seq(prompt);
+        seq.insert(seq.end(), out.begin(), out.end());
+        replay(seq);
+    }
     return out;
+}
+
+// Leaves the model as if every token of seq had been evaluated in order from position 0
+// (no logits): the prompt path of generate over the whole sequence.
+void Model::replay(const std::vector<int>& seq) {
+    reset();
+    prefill(seq, false);
+}
+
+// Model::prefill (model.cpp:355-366): the tokens from the current position on, all but
+// the last in batches (GEMM projections) or as replayed steps without the output head,
+// then the last one as a decode step; returns its logits (empty when not wanted).
+std::vector<float> Model::prefill(const std::vector<int>& tokens, bool want_logits) {
+    if (tokens.empty()) throw std::invalid_argument("Empty prompt");
+    if (tokens.size() > opt_.context - std::min(position_, opt_.context))
+        throw std::runtime_error("Context budget exhausted");
+    for (int t : tokens)
+        if (t < 0 || t >= info_.vocab) throw std::out_of_range("Token ID");
+    const size_t n = tokens.size(), start = position_;
+    backend_->dev_upload(dev_prompt_ + start * sizeof(int), tokens.data(), n * sizeof(int));
+    if (n > 1) {
+        if (opt_.batch_prefill_min && n - 1 >= opt_.batch_prefill_min) {
+            prefill_batched(start, n - 1);
+        } else {
+            set_state(static_cast<int>(start), tokens[0], static_cast<int>(start + n));
+            for (size_t i = 0; i + 1 < n; ++i) {
+                if (opt_.graph) backend_->graph_launch(step_graph(false));
+                else enqueue_step(false);
+            }
+        }
+        position_ = start + n - 1;
+    }
+    return evaluate(tokens[n - 1], want_logits);
 }
 
 }  // namespace emprise

@@ -43,6 +43,8 @@ public:
     std::vector<emprise_hip_trace_record> trace_step(int token);
     // prefill + greedy loop; arrivals[i] = seconds from the first launch to token i
     std::vector<int> generate(const std::vector<int>& prompt, size_t count, std::vector<double>* arrivals);
+    // Model::prefill: tokens from the current position on; the last one's logits
+    std::vector<float> prefill(const std::vector<int>& tokens, bool want_logits = true);
 
 private:
     struct Layer {
@@ -55,9 +57,11 @@ private:
     emprise_weight upload(const std::string& name, uint64_t cols, uint64_t rows);
     emprise_weight upload_vector(const std::string& name, uint64_t n);
     void enqueue_step(bool logits);  // one position, reading token/position from dev_state_
-    // positions [0, count) of `tokens` (already on the device at dev_prompt_) in batches
-    void prefill_batched(size_t count);
+    // positions [start, start + count) of the tokens at dev_prompt_ in batches
+    void prefill_batched(size_t start, size_t count);
     void set_state(int position, int token, int prompt_len);
+    // evaluates seq from position 0 (no logits), leaving position_ = seq.size()
+    void replay(const std::vector<int>& seq);
     emprise_graph step_graph(bool logits);
 
     ModelOptions opt_;

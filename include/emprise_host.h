@@ -64,6 +64,11 @@ emprise_status emprise_model_reset(emprise_model* m);
 /* Model::evaluate (model.cpp:206-259) on the device: one position; logits (vocab
  * floats) may be NULL. */
 emprise_status emprise_model_evaluate(emprise_model* m, int token, float* logits);
+/* Model::prefill (model.cpp:355-366, model.hpp:40-41): evaluates `tokens` from the current
+ * position on -- all but the last in batches (GEMM projections, from 64 tokens) or as
+ * replayed steps, the last as a decode step -- and writes the last position's logits
+ * (vocab floats; may be NULL). The reference prefills in chunks of 4 positions. */
+emprise_status emprise_model_prefill(emprise_model* m, const int* tokens, size_t n, float* logits);
 /* The residual stream after the last evaluated position (Model::last_hidden_raw). */
 emprise_status emprise_model_last_hidden(emprise_model* m, float* hidden);
 

@@ -66,6 +66,8 @@ def lib() -> ctypes.CDLL:
         L.eo_model_generate.argtypes = [vp, ctypes.POINTER(ctypes.c_int), sz, sz, ctypes.POINTER(ctypes.c_int), _fp]
         L.eo_model_last_hidden.restype = i32
         L.eo_model_last_hidden.argtypes = [vp, _fp]
+        L.eo_quantize_q8.argtypes = [_fp, sz, _fp]
+        L.eo_model_set_quantize_activations.argtypes = [vp, i32]
         L.eo_last_error.restype = ctypes.c_char_p
         _lib = L
     return _lib
@@ -135,6 +137,14 @@ def matvec(wtype: int, raw, x: np.ndarray, rows: int) -> np.ndarray:
     return y
 
 
+def quantize_q8(x: np.ndarray) -> np.ndarray:
+    """The --fast-q8 input rule as the CPU check states it (core.cpp:119-125)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().eo_quantize_q8(_f(x), x.size, _f(out))
+    return out
+
+
 def rms(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     y = np.array(x, dtype=np.float32, copy=True)
     w = np.ascontiguousarray(w, dtype=np.float32)
@@ -175,11 +185,13 @@ def attention(heads, kv_heads, head_dim, rotary, rope_base, eps, q_norm, k_norm,
 class Model:
     """The whole CPU decode path over a GGUF file (Model::Impl::evaluate restated)."""
 
-    def __init__(self, path: str, context: int = 4096, threads: int = 0):
+    def __init__(self, path: str, context: int = 4096, threads: int = 0, fast_q8: bool = False):
         err = ctypes.create_string_buffer(512)
         self.m = lib().eo_model_load(str(path).encode(), context, threads, err, 512)
         if not self.m:
             raise RuntimeError(err.value.decode())
+        # --fast-q8: every Q6_K projection sees quantize_q8 of its input
+        lib().eo_model_set_quantize_activations(self.m, 1 if fast_q8 else 0)
         self.vocab = lib().eo_model_vocab(self.m)
         self.hidden = lib().eo_model_hidden(self.m)
 

@@ -290,6 +290,35 @@ int eo_feed_forward(uint32_t gate_type, const uint8_t* gate_w, uint32_t up_type,
     return rc;
 }
 
+/* The nearest fp16 value of a positive float, ties to the even code: the reference
+ * test's own rule (tests/core.cpp:14-21, a monotone search over the finite positive
+ * half codes), used there to form the Q8 check input. */
+static float round_positive_half(float value) {
+    unsigned lo = 0, hi = 0x7bff;
+    while (lo < hi) {
+        const unsigned mid = (lo + hi) / 2;
+        if (eo_half_to_float((uint16_t)mid) < value) lo = mid + 1;
+        else hi = mid;
+    }
+    if (!lo) return 0;
+    const float a = eo_half_to_float((uint16_t)(lo - 1)), b = eo_half_to_float((uint16_t)lo);
+    return value - a < b - value || (value - a == b - value && ((lo - 1) & 1) == 0) ? a : b;
+}
+
+/* --fast-q8 activations as the CPU sees them (cuda.cpp:547-559, checked against the CPU
+ * path in tests/core.cpp:119-125): per 32 inputs s = max|x| / 127, and
+ * x' = round(x / s) * fp16(s) (round: ties away from zero, with the unrounded s). */
+void eo_quantize_q8(const float* x, size_t n, float* out) {
+    for (size_t start = 0; start < n; start += 32) {
+        float scale = 0;
+        for (size_t j = 0; j < 32 && start + j < n; ++j) scale = fmaxf(scale, fabsf(x[start + j]));
+        scale /= 127;
+        const float kept = round_positive_half(scale);
+        for (size_t j = 0; j < 32 && start + j < n; ++j)
+            out[start + j] = scale != 0.f ? roundf(x[start + j] / scale) * kept : 0.f;
+    }
+}
+
 /* ------------------------------------------------------------------------------ */
 /* GGUF reader (gguf.cpp:87-147), resident in RAM like the reference's default.     */
 
@@ -400,6 +429,7 @@ struct eo_model {
     uint32_t tembd, toutput;
     float* output_norm;
     float* last_hidden;
+    int q8; /* --fast-q8: Q6_K projections see quantised inputs */
 };
 
 static const eo_kv* find_kv(const eo_model* m, const char* key) {
@@ -671,6 +701,42 @@ static int linear(uint32_t type, const uint8_t* w, const float* x, size_t cols, 
     return eo_matvec(type, w, eo_encoded_bytes(type, cols * rows), x, cols, y, rows);
 }
 
+/* A projection of the model: with --fast-q8, Q6_K weights see the quantised input
+ * (device_linear, cuda.cpp:707-712: every Q6_K projection, the output head included). */
+static int mlinear(const eo_model* m, uint32_t type, const uint8_t* w, const float* x, size_t cols, float* y,
+                   size_t rows) {
+    if (!m->q8 || type != EO_Q6_K) return linear(type, w, x, cols, y, rows);
+    float* xq = (float*)malloc(cols * sizeof(float));
+    eo_quantize_q8(x, cols, xq);
+    const int rc = linear(type, w, xq, cols, y, rows);
+    free(xq);
+    return rc;
+}
+
+/* Backend::feed_forward (backend.cpp:91-104) with the projections of mlinear. Without
+ * --fast-q8 this is eo_feed_forward exactly. */
+static int model_feed_forward(const eo_model* m, const eo_layer* L, const float* x, float* y) {
+    const size_t H = (size_t)m->hidden, F = (size_t)m->ffn;
+    if (!m->q8) return eo_feed_forward(L->tfg, L->fg, L->tfu, L->fu, L->tfd, L->fd, H, F, x, y);
+    float* g = (float*)malloc(F * sizeof(float));
+    float* u = (float*)malloc(F * sizeof(float));
+    int rc = mlinear(m, L->tfg, L->fg, x, H, g, F);
+    if (!rc) rc = mlinear(m, L->tfu, L->fu, x, H, u, F);
+    if (!rc) {
+        for (size_t i = 0; i < F; ++i) {
+            const float e = expf(-fabsf(g[i]));
+            const float s = g[i] >= 0 ? 1.f / (1.f + e) : e / (1.f + e);
+            g[i] = g[i] * s * u[i];
+        }
+        rc = mlinear(m, L->tfd, L->fd, g, F, y, H);
+    }
+    free(g);
+    free(u);
+    return rc;
+}
+
+void eo_model_set_quantize_activations(eo_model* m, int on) { m->q8 = on != 0; }
+
 /* Model::Impl::evaluate (model.cpp:206-259) with the fused feed-forward default. */
 int eo_model_evaluate(eo_model* m, int token, float* logits) {
     if (m->position >= m->context) { set_err("Context budget exhausted"); return -1; }
@@ -696,34 +762,34 @@ int eo_model_evaluate(eo_model* m, int token, float* logits) {
         eo_rms(nrm, (size_t)H, L->attn_norm, m->eps);
         if (L->recurrent) {
             /* Backend::recurrent_block (backend.cpp:61-77) */
-            if ((rc = linear(L->tqkv, L->qkv, nrm, (size_t)H, b0, (size_t)ch))) break;
-            if ((rc = linear(L->tgate, L->gate, nrm, (size_t)H, b1, (size_t)vd))) break;
-            if ((rc = linear(L->talpha, L->alpha, nrm, (size_t)H, b2, (size_t)m->value_heads))) break;
-            if ((rc = linear(L->tbeta, L->beta, nrm, (size_t)H, b3, (size_t)m->value_heads))) break;
+            if ((rc = mlinear(m, L->tqkv, L->qkv, nrm, (size_t)H, b0, (size_t)ch))) break;
+            if ((rc = mlinear(m, L->tgate, L->gate, nrm, (size_t)H, b1, (size_t)vd))) break;
+            if ((rc = mlinear(m, L->talpha, L->alpha, nrm, (size_t)H, b2, (size_t)m->value_heads))) break;
+            if ((rc = mlinear(m, L->tbeta, L->beta, nrm, (size_t)H, b3, (size_t)m->value_heads))) break;
             eo_delta_net(m->key_heads, m->value_heads, m->state_dim, m->conv_width, m->eps, b0, b1, b2, b3,
                          L->conv, L->ssm_a, L->dt, L->ssm_norm, S->conv, S->rec, b4);
-            if ((rc = linear(L->tout, L->out, b4, (size_t)vd, attn, (size_t)H))) break;
+            if ((rc = mlinear(m, L->tout, L->out, b4, (size_t)vd, attn, (size_t)H))) break;
         } else {
             /* attention (model.cpp:161-164) */
-            if ((rc = linear(L->tq, L->q, nrm, (size_t)H, b0, (size_t)qd))) break;
-            if ((rc = linear(L->tk, L->k, nrm, (size_t)H, b1, (size_t)kvd))) break;
-            if ((rc = linear(L->tv, L->v, nrm, (size_t)H, b2, (size_t)kvd))) break;
+            if ((rc = mlinear(m, L->tq, L->q, nrm, (size_t)H, b0, (size_t)qd))) break;
+            if ((rc = mlinear(m, L->tk, L->k, nrm, (size_t)H, b1, (size_t)kvd))) break;
+            if ((rc = mlinear(m, L->tv, L->v, nrm, (size_t)H, b2, (size_t)kvd))) break;
             S->length += 1;
             eo_attention(m->heads, m->kv_heads, m->head_dim, m->rotary, m->rope_base, m->eps, L->q_norm, L->k_norm,
                          b0, b1, b2, S->keys, S->values, S->length, (int)m->position, b4);
-            if ((rc = linear(L->to, L->o, b4, (size_t)m->heads * m->head_dim, attn, (size_t)H))) break;
+            if ((rc = mlinear(m, L->to, L->o, b4, (size_t)m->heads * m->head_dim, attn, (size_t)H))) break;
         }
         for (int i = 0; i < H; ++i) x[i] += attn[i];
         memcpy(nrm, x, (size_t)H * sizeof(float));
         eo_rms(nrm, (size_t)H, L->post_norm, m->eps);
-        if ((rc = eo_feed_forward(L->tfg, L->fg, L->tfu, L->fu, L->tfd, L->fd, (size_t)H, (size_t)m->ffn, nrm, attn))) break;
+        if ((rc = model_feed_forward(m, L, nrm, attn))) break;
         for (int i = 0; i < H; ++i) x[i] += attn[i];
     }
     if (rc == 0) {
         memcpy(m->last_hidden, x, (size_t)H * sizeof(float));
         if (logits) {
             eo_rms(x, (size_t)H, m->output_norm, m->eps);
-            rc = linear(m->toutput, m->output, x, (size_t)H, logits, (size_t)m->vocab);
+            rc = mlinear(m, m->toutput, m->output, x, (size_t)H, logits, (size_t)m->vocab);
         }
         if (rc == 0) ++m->position;
     }

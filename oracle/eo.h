@@ -26,6 +26,9 @@
  *                      of v, fp64 brute force
  *   eo_model_*         composition of the above; teacher-forced token agreement
  *                      with a step-by-step composition of _ref ops
+ *   eo_quantize_q8     core.cpp:119-125's construction of the checked input; fp16(s) by
+ *                      the test's monotone search (core.cpp:14-21), tested against numpy's
+ *                      float16 rounding and the GPU's standalone quantiser bit for bit
  */
 #ifndef EMPRISE_ORACLE_H
 #define EMPRISE_ORACLE_H
@@ -73,6 +76,10 @@ int eo_feed_forward(uint32_t gate_type, const uint8_t* gate_w, uint32_t up_type,
                     uint32_t down_type, const uint8_t* down_w, size_t hidden, size_t ffn,
                     const float* x, float* y);
 
+/* --fast-q8 input rule (cuda.cpp:547-559 as checked in core.cpp:119-125): per 32 values
+ * s = max|x|/127, out = round(x/s) * fp16(s). */
+void eo_quantize_q8(const float* x, size_t n, float* out);
+
 /* ---- whole model (GGUF file in, logits out) ---- */
 typedef struct eo_model eo_model;
 /* threads = 0 keeps the OpenMP default. Returns NULL and fills err on failure. */
@@ -81,6 +88,9 @@ void eo_model_free(eo_model* m);
 int eo_model_vocab(const eo_model* m);
 int eo_model_hidden(const eo_model* m);
 void eo_model_reset(eo_model* m);
+/* --fast-q8: every Q6_K projection (output head included) sees eo_quantize_q8 of its
+ * input, the CPU statement of the reference's device_linear in fast mode (cuda.cpp:707-712). */
+void eo_model_set_quantize_activations(eo_model* m, int on);
 /* Model::Impl::evaluate (model.cpp:206-259). logits may be NULL. Returns 0 or -1. */
 int eo_model_evaluate(eo_model* m, int token, float* logits);
 /* Model::generate (model.cpp:488-503) with the prompt prefilled position by position.

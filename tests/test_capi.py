@@ -101,3 +101,26 @@ def test_synth_prompt_ids():
 def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+REF_INCLUDE = Path("/root/reference/v1.1/include")
+
+
+@pytest.mark.skipif(not REF_INCLUDE.exists(), reason="reference tree not mounted")
+def test_integration_adapter_compiles(tmp_path):
+    """The reference-side adapter in INTEGRATION.md (section 1) compiles against the
+    reference's Backend interface (backend.hpp) and this repository's C ABI header."""
+    import shutil
+    text = (ROOT / "INTEGRATION.md").read_text()
+    section = text[text.index("## 1. The adapter"):text.index("## 2. Factory")]
+    code = re.search(r"```cpp\n(.*?)```", section, flags=re.S).group(1)
+    src = tmp_path / "hip_backend.cpp"
+    src.write_text(code)
+    gxx = shutil.which("g++")
+    if not gxx:
+        pytest.skip("g++ missing")
+    r = subprocess.run([gxx, "-std=c++20", "-fsyntax-only", "-Wall", "-Wextra", f"-I{REF_INCLUDE}",
+                        f"-I{REF_INCLUDE.parent / 'third_party'}", f"-I{ROOT / 'include'}", str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-4000:]
+    assert "delta_net(Gguf& m, const DeltaNet& p) override" in code

@@ -265,7 +265,8 @@ def test_feed_forward(backend, wtype):
         backend.weight_free(w)
 
 
-@pytest.mark.parametrize("rows,cols", [(256, 4096), (4096, 4096), (1024, 12288)])
+@pytest.mark.parametrize("rows,cols", [(256, 4096), (4096, 4096), (1024, 12288), (12288, 4096), (4096, 12288),
+                                       (151936, 4096), (64, 512), (1536, 512), (512, 1536)])
 def test_q8_path(backend_q8, rows, cols):
     raw, x, got = _run_linear(backend_q8, Q6_K, rows, cols, seed=rows + cols)
     ref = oracle.matvec(Q6_K, raw, quantize_like_reference(x), rows)
@@ -309,3 +310,83 @@ def test_budget_exhaustion():
         with pytest.raises(EmpriseError) as e:
             be.upload_weight(Q6_K, 4096, 1, b"\0" * 3360)
         assert e.value.status == ENOMEM
+
+
+def _q8_check(got, raw, rows, cols, xin):
+    """The Q8 bar of core.cpp:119-129 (CPU matvec on round(x/s)*fp16(s), within
+    1e-3 + 1e-4|ref|), plus one quantum of the input (s = amax/127 of its 32-block) times
+    the largest weight of each row: the GPU quantises its own FP32 input, which can differ
+    from the CPU's in the last bits and round one step the other way."""
+    ref = oracle.matvec(Q6_K, raw, quantize_like_reference(xin), rows)
+    w = np.abs(oracle.dequantize(Q6_K, raw, rows * cols).reshape(rows, cols))
+    step = np.repeat(np.max(np.abs(xin.reshape(-1, 32)), axis=1) / 127, 32)
+    flip = np.max(w * step[None, :], axis=1)
+    bad = np.abs(got - ref) > 1e-3 + 1e-4 * np.abs(ref) + flip
+    assert not bad.any(), (int(bad.sum()), float(np.max(np.abs(got - ref))))
+    return ref
+
+
+@pytest.mark.parametrize("rows,cols", [(1536, 512), (1024, 4096)])
+def test_linear_norm_q8(backend_q8, rows, cols):
+    """--fast-q8 with the residual add + RMSNorm prologue: the normalised input is what
+    gets quantised (device_linear after dev_add + dev_rmsnorm, cuda.cpp:707-712)."""
+    rng = np.random.default_rng(rows + cols)
+    eps = 1e-6
+    raw = matrix(rng, Q6_K, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    delta = rng.standard_normal(cols).astype(np.float32)
+    nw = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
+    be = backend_q8
+    w, nwd = be.upload_weight(Q6_K, cols, rows, raw), be.vector(nw)
+    xd, dd, xo, yd = be.to_device(x), be.to_device(delta), be.alloc(cols * 4), be.alloc(rows * 4)
+    be.linear_norm(Input(xd, dd, xo, nwd, eps), [w], [yd])
+    _q8_check(be.download(yd, rows), raw, rows, cols, oracle.rms(x + delta, nw, eps))
+    for b in (xd, dd, xo, yd):
+        be.free(b)
+    be.weight_free(w)
+
+
+@pytest.mark.parametrize("hidden,ffn", [(512, 1536), (4096, 12288)])
+def test_feed_forward_q8(backend_q8, hidden, ffn):
+    """--fast-q8 SwiGLU FFN (cuda.cpp:897-927): gate and up on the quantised input, down
+    on the quantised SwiGLU output."""
+    rng = np.random.default_rng(hidden + 7)
+    be = backend_q8
+    graw, uraw, draw = matrix(rng, Q6_K, ffn, hidden), matrix(rng, Q6_K, ffn, hidden), matrix(rng, Q6_K, hidden, ffn)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    g, u, d = (be.upload_weight(Q6_K, c, r, raw) for r, c, raw in ((ffn, hidden, graw), (ffn, hidden, uraw),
+                                                                     (hidden, ffn, draw)))
+    xd, yd = be.to_device(x), be.alloc(hidden * 4)
+    be.feed_forward(g, u, d, xd, yd)
+    xq = quantize_like_reference(x)
+    gr, ur = oracle.matvec(Q6_K, graw, xq, ffn), oracle.matvec(Q6_K, uraw, xq, ffn)
+    e = np.exp(-np.abs(gr))
+    s = np.where(gr >= 0, 1 / (1 + e), e / (1 + e)).astype(np.float32)
+    h = (gr * s * ur).astype(np.float32)
+    _q8_check(be.download(yd, hidden), draw, hidden, ffn, h)
+    for wt in (g, u, d):
+        be.weight_free(wt)
+    be.free(xd)
+    be.free(yd)
+
+
+@pytest.mark.parametrize("vocab,hidden", [(4096, 512), (151936, 4096)])
+def test_lm_head_q8(backend_q8, vocab, hidden):
+    """--fast-q8 output head: RMSNorm of x + delta, quantised, Q6_K matvec, argmax."""
+    rng = np.random.default_rng(vocab)
+    be = backend_q8
+    eps = 1e-6
+    raw = matrix(rng, Q6_K, vocab, hidden)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    delta = rng.standard_normal(hidden).astype(np.float32)
+    nw = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32)
+    w, nwd = be.upload_weight(Q6_K, hidden, vocab, raw), be.vector(nw)
+    xd, dd, xo = be.to_device(x), be.to_device(delta), be.alloc(hidden * 4)
+    ld, idx = be.alloc(vocab * 4), be.alloc(4)
+    be.lm_head(Input(xd, dd, xo, nwd, eps), w, ld, idx)
+    got = be.download(ld, vocab)
+    _q8_check(got, raw, vocab, hidden, oracle.rms(x + delta, nw, eps))
+    assert int(be.download(idx, 1, np.int32)[0]) == int(np.argmax(got))
+    for b in (xd, dd, xo, ld, idx):
+        be.free(b)
+    be.weight_free(w)

@@ -101,21 +101,89 @@ def test_evaluate_rejects_bad_tokens(tiny_path):
         m.generate([1, 2], 6)
 
 
-def test_fast_q8_tiny_runs_and_tracks_fp32(tiny_path):
-    """--fast-q8: same weights with Q8 activations (Q6_K projections only)."""
-    prompt = synth_prompt(5, TINY["vocab"], 16)
+def test_generate_then_evaluate_continues_like_reference(tiny_path):
+    """After generate the model sits where the reference's does (model.cpp:497-502: the
+    prompt and every emitted token but the last evaluated), so evaluating the last token
+    continues the same sequence: its logits match the oracle's continuation."""
+    prompt = synth_prompt(11, TINY["vocab"], 20)
+    ref = oracle.Model(tiny_path, context=512)
+    ref_tokens, margins = ref.generate(prompt, 12)
+    want = ref.evaluate(ref_tokens[-1])
+    for batch in (8, -1):  # batched prefill and per-position prefill
+        with Model(tiny_path, context=512, batch_prefill=batch) as m:
+            tokens, _ = m.generate(prompt, 12)
+            assert _greedy_agreement(tokens, ref_tokens, margins) == 12
+            got = m.evaluate(tokens[-1])
+        err = np.max(np.abs(got.astype(np.float64) - want))
+        assert err <= 2e-4 * np.max(np.abs(want)), err
+        assert int(np.argmax(got)) == int(np.argmax(want))
+
+
+def test_generate_stops_at_eos_like_reference(tmp_path):
+    """EOS ends generation without emitting it (model.cpp:500), and the model is left
+    where the reference leaves it: the prompt and the emitted tokens evaluated."""
+    prompt = synth_prompt(12, TINY["vocab"], 20)
+    base = tmp_path / "base.gguf"
+    synth_write(base, seed=0, **TINY)
+    ref_tokens, _ = oracle.Model(str(base), context=512).generate(prompt, 10)
+    stop = next(i for i in range(3, 10) if ref_tokens[i] not in ref_tokens[:i])
+    eos = ref_tokens[stop]
+    path = tmp_path / "eos.gguf"
+    synth_write(path, seed=0, **dict(TINY, eos=eos))  # same weights, EOS = a later pick
+    ref = oracle.Model(str(path), context=512)
+    r_tokens, _ = ref.generate(prompt, 10)
+    assert r_tokens == ref_tokens[:stop]
+    want = ref.evaluate(r_tokens[-1])
+    with Model(str(path), context=512) as m:
+        tokens, arrivals = m.generate(prompt, 10)
+        assert tokens == r_tokens and len(arrivals) == stop
+        got = m.evaluate(tokens[-1])
+    assert np.max(np.abs(got.astype(np.float64) - want)) <= 2e-4 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("batch", [8, -1])
+def test_prefill_matches_oracle(tiny_path, batch):
+    """Model::prefill (model.cpp:355-366) from position 0 and again from the position it
+    left: logits of each chunk's last position against the oracle's evaluate."""
+    toks = synth_prompt(13, TINY["vocab"], 90)
+    ref = oracle.Model(tiny_path, context=512)
+    with Model(tiny_path, context=512, batch_prefill=batch) as m:
+        for lo, hi in ((0, 70), (70, 90)):
+            got = m.prefill(toks[lo:hi])
+            for t in toks[lo:hi]:
+                want = ref.evaluate(t)
+            assert np.max(np.abs(got.astype(np.float64) - want)) <= 2e-4 * np.max(np.abs(want)), (lo, hi)
+
+
+def test_fast_q8_tiny_matches_oracle_q8(tiny_path):
+    """--fast-q8 end to end against the oracle's Q8 mode (every Q6_K projection, output
+    head included, on round(x/s)*fp16(s) inputs; core.cpp:119-125, cuda.cpp:707-712),
+    teacher-forced.
+
+    The op-level Q8 bar is tight (test_gpu_matvec.py: q8_path, linear_norm_q8,
+    feed_forward_q8, lm_head_q8; test_gpu_ops.py: recurrent_block_q8). End to end it
+    cannot be: the GPU quantises its own FP32 activations, which differ from the CPU's in
+    the last bits, so now and then an input rounds one quantum (amax/127) the other way;
+    that moves the next layer's inputs by ~1e-4, and from there many inputs cross a
+    rounding boundary. A one-layer model agrees to 4e-7 except at such a flip (1.5e-3);
+    four layers drift ~1-2% apart, against ~4% between the oracle's Q8 and FP32 paths.
+    Bar: logits within 5e-2 relative L2 of the oracle's Q8, closer to it than to the
+    oracle's FP32 logits on average, and the same pick wherever the Q8 margin exceeds 0.1."""
+    prompt = synth_prompt(5, TINY["vocab"], 24)
+    ref = oracle.Model(tiny_path, context=512, fast_q8=True)
+    ref32 = oracle.Model(tiny_path, context=512)
+    rels, rels32 = [], []
     with Model(tiny_path, context=512, fast_q8=True) as m:
         assert "Q8" in m.backend_name
-        logits_q8 = [m.evaluate(t) for t in prompt]
-    with Model(tiny_path, context=512) as m:
-        logits_fp = [m.evaluate(t) for t in prompt]
-    # Q8 activations are a lossy path with no CPU counterpart in the reference; its op
-    # level bar is in test_gpu_matvec. End to end it must stay close to FP32 and pick
-    # the same token wherever FP32's top-2 margin is wide.
-    for a, b in zip(logits_q8, logits_fp):
-        assert np.all(np.isfinite(a))
-        rel = np.linalg.norm(a - b) / np.linalg.norm(b)
-        assert rel < 0.15, rel
-        top = np.sort(b)[-2:]
-        if top[1] - top[0] > 0.5:
-            assert int(np.argmax(a)) == int(np.argmax(b))
+        for pos, t in enumerate(prompt):
+            want, want32 = ref.evaluate(t), ref32.evaluate(t)
+            got = m.evaluate(t).astype(np.float64)
+            rels.append(float(np.linalg.norm(got - want) / np.linalg.norm(want)))
+            rels32.append(float(np.linalg.norm(got - want32) / np.linalg.norm(want32)))
+            assert rels[-1] <= 5e-2, (pos, rels[-1])
+            top = np.sort(want)[-2:]
+            if top[1] - top[0] > 0.1:
+                assert int(np.argmax(got)) == int(np.argmax(want)), pos
+    print(f"fast-q8 tiny: relative L2 to the oracle's Q8 mean {np.mean(rels):.3e} max {max(rels):.3e}; "
+          f"to its FP32 path mean {np.mean(rels32):.3e}")
+    assert np.mean(rels) < np.mean(rels32)

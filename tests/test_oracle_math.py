@@ -171,3 +171,53 @@ def test_delta_net_conv_history_shifts():
         _dn(kh, vh, sd, cw, qkv, np.ones(sd, np.float32), np.zeros(1, np.float32), np.zeros(1, np.float32), ones,
             np.full(1, -1.0, np.float32), np.zeros(1, np.float32), np.ones(sd, np.float32), cs, rs)
     assert np.array_equal(cs.reshape(ch, cw)[0], [2.0, 3.0, 4.0])
+
+
+def test_attention_softmax_temperature_two_keys():
+    """Two keys with a closed-form score pins the 1/sqrt(head_dim) temperature
+    (model.cpp:143-148): q and the keys are axis vectors, so after the per-head RMSNorm
+    (unit weights) q.k is known exactly and the softmax weight of key 0 is
+    e^s / (e^s + 1) with s = q.k / sqrt(hd). A temperature of 1 or 1/hd misses it."""
+    eps = 1e-6
+    for hd in (4, 16):
+        qg = np.zeros(2 * hd, np.float32)
+        qg[2] = 1.0  # q = e_2; gate 0 -> sigmoid 1/2
+        k_new = np.zeros(hd, np.float32)
+        k_new[3] = 1.0  # new key e_3, orthogonal to q
+        keys = np.zeros((2, hd), np.float32)
+        values = np.zeros((2, hd), np.float32)
+        norm = 1 / np.sqrt(1 / hd + eps)  # RMSNorm scale of an axis vector
+        keys[0, 2] = norm  # key 0 already stored in its normalised form
+        values[0, 0] = 1.0
+        v_new = np.zeros(hd, np.float32)
+        v_new[1] = 1.0
+        out = oracle.attention(1, 1, hd, 0, 1e7, eps, np.ones(hd, np.float32), np.ones(hd, np.float32), qg, k_new,
+                               v_new, keys, values, 2, 1)
+        s = norm * norm / np.sqrt(hd)
+        p0 = np.exp(s) / (np.exp(s) + 1)
+        want = np.zeros(hd)
+        want[0], want[1] = 0.5 * p0, 0.5 * (1 - p0)
+        assert np.allclose(out, want, rtol=1e-5, atol=1e-7), (hd, out[:2], want[:2])
+        for wrong in (s * np.sqrt(hd), s / np.sqrt(hd)):
+            pw = np.exp(wrong) / (np.exp(wrong) + 1)
+            assert abs(out[0] - 0.5 * pw) > 1e-3
+
+
+def test_quantize_q8_matches_core_rule():
+    """eo_quantize_q8 (the fast-q8 input of core.cpp:119-125) against the numpy statement
+    of the same rule (tests/synth.py: float16 cast for fp16(s), ties away from zero by
+    hand), bit for bit, over blocks that hit exact .5 ties, zero blocks, fp16-subnormal
+    scales and large values; plus closed forms."""
+    from synth import quantize_like_reference
+    rng = np.random.default_rng(4)
+    blocks = [rng.standard_normal(32) * 10.0 ** rng.uniform(-9, 4) for _ in range(200)]
+    tie = np.arange(32, dtype=np.float64) - 15.5
+    tie[0] = 127.0  # s = 1: every other value is an exact .5 tie
+    blocks += [np.zeros(32), tie, -tie, np.full(32, 1e-9), np.full(32, 3e4)]
+    x = np.concatenate(blocks).astype(np.float32)
+    got = oracle.quantize_q8(x)
+    assert np.array_equal(got.view(np.uint32), quantize_like_reference(x).view(np.uint32))
+    # closed forms: s = 1 rounds half away from zero; a zero block stays zero
+    t = got[201 * 32:202 * 32]
+    assert t[1] == -15.0 and t[16] == 1.0 and t[15] == -1.0 and t[31] == 16.0
+    assert not got[200 * 32:201 * 32].any()
