@@ -97,6 +97,7 @@ def hip_lib() -> ctypes.CDLL:
         "emprise_hip_argmax": (st, [vp, u64, i32, u64]),
         "emprise_hip_quantize_q8": (st, [vp, u64, i32, u64, u64]),
         "emprise_hip_delta_net": (st, [vp, vp]),
+        "emprise_hip_delta_net_noalloc": (st, [vp, vp]),
         "emprise_hip_delta_net_batch": (st, [vp, vp, i32, u64, u64]),
         "emprise_hip_recurrent": (st, [vp, vp, vp, u64, u64]),
         "emprise_hip_attention": (st, [vp, vp, u64, u64]),
@@ -303,6 +304,10 @@ class HipBackend:
 
     def delta_net(self, p: DeltaNetParams):
         self._check(self.lib.emprise_hip_delta_net(self.h, ctypes.byref(p)))
+
+    def delta_net_noalloc(self, p: DeltaNetParams):
+        """emprise_hip_delta_net_noalloc: delta_net with no device allocation (fixed scratch)."""
+        self._check(self.lib.emprise_hip_delta_net_noalloc(self.h, ctypes.byref(p)))
 
     def delta_net_batch(self, p: DeltaNetParams, count: int, stride: int, out_stride: int):
         """delta_net over `count` positions: row t of qkv/gate/alpha/beta at t*stride floats,

@@ -100,8 +100,17 @@ struct StepEmbed {
 
 }  // namespace
 
+// Scratch of emprise_hip_delta_net_noalloc: the conv'd channels of one GDN step, in a
+// fixed device array instead of library-allocated memory. 65536 floats (256 KiB) cover
+// (2*key_heads + value_heads)*state_dim up to 65536 (the 9B shape has 8192). Each GPU
+// the library runs on holds its own copy until the process ends; host code reaches it
+// only through the address hipGetSymbolAddress returns for the current device.
+constexpr int kNoAllocScratchFloats = 65536;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
 struct emprise_hip {
     int device = 0;
+    float* noalloc_scratch = nullptr;  // this device's address of `scratch`
     hipStream_t stream = nullptr;
     uint64_t budget = 0, used = 0;
     bool q8 = false;
@@ -545,8 +554,14 @@ emprise_status emprise_hip_create(int device, uint64_t weight_budget, int quanti
     HIP_TRY(hipGetDeviceProperties(&prop, device));
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(EMPRISE_EDEVICE, "built for gfx950, found %s", prop.gcnArchName);
+    // the no-alloc entry point's scratch: this device's copy of the array
+    void* scratch_addr = nullptr;
+    const hipError_t se = hipGetSymbolAddress(&scratch_addr, HIP_SYMBOL(scratch));
+    if (se != hipSuccess || !scratch_addr)
+        return fail(EMPRISE_EDEVICE, "scratch symbol address: %s", hipGetErrorString(se));
     auto* h = new emprise_hip();
     h->device = device;
+    h->noalloc_scratch = static_cast<float*>(scratch_addr);
     h->q8 = quantize_activations != 0;
     hipError_t e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
@@ -975,6 +990,45 @@ emprise_status emprise_hip_delta_net(emprise_hip* h, const emprise_hip_delta_net
     g.state = reinterpret_cast<float*>(p->rec_state);
     g.out = reinterpret_cast<float*>(p->out);
     return traced(h, "gdn_step", gdn_bytes(g), [&] { return launch_gdn(g, h->stream); });
+}
+
+emprise_status emprise_hip_delta_net_noalloc(emprise_hip* h, const emprise_hip_delta_net_params* p) {
+    if (!h || !p) return fail(EMPRISE_EINVAL, "null argument");
+    const int kd = p->key_heads * p->state_dim, vd = p->value_heads * p->state_dim, ch = 2 * kd + vd;
+    if (p->key_heads < 1 || p->value_heads < 1 || p->state_dim < 1 || ch > kNoAllocScratchFloats)
+        return fail(EMPRISE_EINVAL, "delta_net_noalloc: %d channels exceed the %d-float scratch", ch,
+                    kNoAllocScratchFloats);
+    const Weight *conv = h->weight(p->conv), *a = h->weight(p->ssm_a), *dt = h->weight(p->dt), *nw = h->weight(p->norm);
+    if (p->value_heads % p->key_heads || (p->state_dim != 64 && p->state_dim != 128) || p->conv_width < 1 || !conv ||
+        !a || !dt || !nw || conv->rows * conv->cols != (uint64_t)ch * p->conv_width ||
+        a->rows * a->cols != (uint64_t)p->value_heads || dt->rows * dt->cols != (uint64_t)p->value_heads ||
+        nw->rows * nw->cols != (uint64_t)p->state_dim || conv->type != kF32 || a->type != kF32 || dt->type != kF32 ||
+        nw->type != kF32)
+        return fail(EMPRISE_EINVAL, "Recurrent projection dimensions");
+    if (!p->qkv || !p->gate || !p->alpha || !p->beta || !p->conv_state || !p->rec_state || !p->out)
+        return fail(EMPRISE_EINVAL, "null buffer");
+    if (h->recording) return fail(EMPRISE_ESTATE, "delta_net_noalloc is not recorded into step programs");
+    // the conv kernel writes all ch channels of the scratch before the state update reads
+    // them, so nothing carried over from an earlier call is read
+    float* conv_out = h->noalloc_scratch;
+    TRY(launched(launch_delta_conv(reinterpret_cast<const float*>(p->qkv), reinterpret_cast<const float*>(conv->dev),
+                                   reinterpret_cast<float*>(p->conv_state), conv_out, ch, p->conv_width, h->stream)));
+    GdnArgs g{};
+    g.key_heads = p->key_heads;
+    g.value_heads = p->value_heads;
+    g.state_dim = p->state_dim;
+    g.conv_width = p->conv_width;
+    g.eps = p->eps;
+    g.qkv = conv_out;
+    g.gate = reinterpret_cast<const float*>(p->gate);
+    g.alpha = reinterpret_cast<const float*>(p->alpha);
+    g.beta = reinterpret_cast<const float*>(p->beta);
+    g.ssm_a = reinterpret_cast<const float*>(a->dev);
+    g.dt = reinterpret_cast<const float*>(dt->dev);
+    g.norm = reinterpret_cast<const float*>(nw->dev);
+    g.state = reinterpret_cast<float*>(p->rec_state);
+    g.out = reinterpret_cast<float*>(p->out);
+    return launched(launch_gdn(g, h->stream));
 }
 
 emprise_status emprise_hip_delta_net_batch(emprise_hip* h, const emprise_hip_delta_net_params* p, int count,

@@ -188,6 +188,17 @@ typedef struct {
  * (cuda.cpp:417-479): causal conv1d + SiLU, q/k L2 norm, gated delta-rule update,
  * per-head RMSNorm x SiLU(gate). qkv is not modified. */
 emprise_status emprise_hip_delta_net(emprise_hip* h, const emprise_hip_delta_net_params* p);
+/* No counterpart in the reference: emprise_hip_delta_net for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). It allocates nothing: the conv'd channels of the step go to a
+ * fixed device array of 65536 floats (256 KiB) that each GPU the library runs on holds
+ * until the process ends, so (2*key_heads + value_heads)*state_dim may not exceed 65536
+ * (EMPRISE_EINVAL otherwise). The caller passes every input, output and state buffer as
+ * for emprise_hip_delta_net, and gets the same results bit for bit. Every call on one
+ * GPU shares that array: calls that overlap on one GPU (several streams or handles)
+ * race. Each call writes all the channels it reads before reading them, so nothing
+ * needs clearing between calls. Not recordable into step programs (EMPRISE_ESTATE). */
+emprise_status emprise_hip_delta_net_noalloc(emprise_hip* h, const emprise_hip_delta_net_params* p);
 /* Backend::delta_net over `count` consecutive positions, for the batched prompt prefill
  * (the reference runs it position by position inside its 4-position prefill batches,
  * model.cpp:355-366): qkv, gate, alpha and beta are the rows of position 0, the rows of
