@@ -67,8 +67,35 @@ def dominant_kernel(trace):
     return name, launches, nbytes / launches, ms / launches, ms / total_ms, agg
 
 
-def cpu_baseline(path: Path, seconds: float, context: int):
-    """The reference's OpenMP CPU decode (restated in oracle/) on a bounded sample."""
+def cpu_info():
+    """CPU model name and physical core count of this host (from /proc/cpuinfo)."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            k, _, val = line.partition(":")
+            k, val = k.strip(), val.strip()
+            if k == "model name" and model == "unknown":
+                model = val
+            elif k == "physical id":
+                phys = val
+            elif k == "core id":
+                core = val
+            elif not k and phys is not None and core is not None:
+                cores.add((phys, core))
+                phys = core = None
+        if phys is not None and core is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    return model, len(cores) or (os.cpu_count() or 1)
+
+
+def cpu_baseline(path: Path, seconds: float, context: int, position: int):
+    """The reference's OpenMP CPU decode (restated in oracle/) on a bounded sample of the
+    GPU run's positions: a 4-token prompt, then the model jumps to `position` (zeroed K/V
+    rows there, so attention spans position + 1 rows as after the GPU run's prompt) and
+    decodes greedily for ~`seconds`."""
     import oracle
     threads = min(16, os.cpu_count() or 1)  # the reference default, model.cpp:51-52
     m = oracle.Model(str(path), context=context, threads=threads)
@@ -77,6 +104,7 @@ def cpu_baseline(path: Path, seconds: float, context: int):
     logits = None
     for t in prompt:
         logits = m.evaluate(t)
+    m.seek(position)
     arrivals, tok = [], int(logits.argmax())
     t0 = time.perf_counter()
     while True:
@@ -87,10 +115,13 @@ def cpu_baseline(path: Path, seconds: float, context: int):
             break
     m.close()
     rate = (len(arrivals) - 1) / (arrivals[-1] - arrivals[0])
+    model, phys = cpu_info()
     return {"value": round(rate, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{len(arrivals)} greedy decode steps of the same 9B-shape Q6_K model after a 4-token "
-                      f"prompt (positions 4-{4 + len(arrivals)}), oracle/ C restatement of the reference "
-                      f"CPU path, OpenMP {threads} threads"}
+            "cpu_model": model, "physical_cores": phys,
+            "sample": f"{len(arrivals)} greedy decode steps of the same 9B-shape model at positions "
+                      f"{position}-{position + len(arrivals) - 1} (the GPU run's), oracle/ C restatement of the "
+                      f"reference CPU path, OpenMP {threads} threads (the reference's default min(16, hardware "
+                      f"threads)) on {model}, {phys} physical cores"}
 
 
 def copy_probe(mib: int):
@@ -374,7 +405,7 @@ def main():
     cpu = None
     if not args.no_cpu and args.model.startswith("9b"):
         log(f"cpu baseline: ~{args.cpu_seconds:.0f}s sample")
-        cpu = cpu_baseline(path, args.cpu_seconds, args.context)
+        cpu = cpu_baseline(path, args.cpu_seconds, args.context, args.prompt)
         log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
 
     workload = {"9b_q6k": "9B-shape qwen35 Q6_K greedy decode, batch 1",

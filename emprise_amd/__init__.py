@@ -448,6 +448,8 @@ def host_lib() -> ctypes.CDLL:
     lib.emprise_model_evaluate.argtypes = [vp, ctypes.c_int, P(ctypes.c_float)]
     lib.emprise_model_last_hidden.restype = ctypes.c_int
     lib.emprise_model_last_hidden.argtypes = [vp, P(ctypes.c_float)]
+    lib.emprise_gguf_inspect.restype = ctypes.c_int
+    lib.emprise_gguf_inspect.argtypes = [ctypes.c_char_p, P(ctypes.c_uint64), P(ctypes.c_uint64)]
     lib.emprise_model_prefill.restype = ctypes.c_int
     lib.emprise_model_prefill.argtypes = [vp, P(ctypes.c_int), ctypes.c_size_t, P(ctypes.c_float)]
     lib.emprise_model_generate.restype = ctypes.c_int
@@ -475,6 +477,13 @@ def synth_write(path, seed: int = 0, matrix_type: int = Q6_K, q4_k_m_mix: bool =
     """Writes a deterministic synthetic qwen35 GGUF (see emprise_synth_write)."""
     c = SynthConfig(seed=seed, matrix_type=matrix_type, q4_k_m_mix=int(q4_k_m_mix), **shape)
     _host_check(host_lib().emprise_synth_write(ctypes.byref(c), str(path).encode()))
+
+
+def gguf_inspect(path):
+    """Validates a GGUF file without a device: (tensor count, metadata key count)."""
+    t, m = ctypes.c_uint64(), ctypes.c_uint64()
+    _host_check(host_lib().emprise_gguf_inspect(str(path).encode(), ctypes.byref(t), ctypes.byref(m)))
+    return t.value, m.value
 
 
 def synth_prompt(seed: int, vocab: int, n: int) -> list:

@@ -7,6 +7,7 @@
 #include <string>
 
 #include "emprise_host.h"
+#include "gguf.hpp"
 #include "model.hpp"
 
 namespace emprise {
@@ -45,6 +46,22 @@ template <class F> emprise_status guarded(F&& f) {
 extern "C" {
 
 const char* emprise_host_last_error(void) { return g_error.c_str(); }
+
+emprise_status emprise_gguf_inspect(const char* path, uint64_t* tensors, uint64_t* metadata) {
+    if (!path) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    try {
+        emprise::Gguf g(path);
+        if (tensors) *tensors = g.tensors().size();
+        if (metadata) *metadata = g.metadata_count();
+        return EMPRISE_OK;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return EMPRISE_EINVAL;
+    }
+}
 
 emprise_status emprise_model_open(const emprise_model_options* o, emprise_model** out) {
     if (!o || !o->path || !out) {

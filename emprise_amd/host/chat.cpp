@@ -30,6 +30,24 @@ std::vector<int> parse_ids(const std::string& s) {
     return ids;
 }
 
+// A JSON string literal: quotes, backslashes and control characters escaped.
+std::string json_string(const std::string& s) {
+    std::string o = "\"";
+    for (unsigned char c : s) {
+        if (c == '"' || c == '\\') {
+            o += '\\';
+            o += static_cast<char>(c);
+        } else if (c < 0x20) {
+            char buf[8];
+            std::snprintf(buf, sizeof buf, "\\u%04x", c);
+            o += buf;
+        } else {
+            o += static_cast<char>(c);
+        }
+    }
+    return o + "\"";
+}
+
 template <class T> std::string json_list(const std::vector<T>& v) {
     std::ostringstream o;
     o.precision(9);
@@ -104,16 +122,22 @@ int main(int argc, char** argv) {
         std::cerr << "Load: " << load << "s; first token after load: " << first << "s; generated: " << emitted
                   << "; decode: " << rate << " tokens/s (" << 100.0 * roofline << "% of the 8 TB/s weight roofline)\n";
         if (!report_file.empty()) {
+            // The reference's --report fields (chat.cpp:77-84), then this build's roofline.
+            // text: token ids are not detokenised here. matrix_seconds / matrix_calls /
+            // non_matrix_seconds are the reference's host timers around each backend call;
+            // the device path replays one graph per token and has no such calls: 0.
             std::ofstream f(report_file);
             if (!f) throw std::runtime_error("Cannot write report");
             f.precision(9);
-            f << "{\n  \"engine\": \"emprise mi355x\",\n  \"backend\": \"" << emprise_model_backend_name(m)
-              << "\",\n  \"model\": \"" << model << "\",\n  \"prompt_tokens\": " << json_list(prompt)
+            f << "{\n  \"engine\": \"emprise mi355x\",\n  \"backend\": " << json_string(emprise_model_backend_name(m))
+              << ",\n  \"model\": " << json_string(model) << ",\n  \"prompt_tokens\": " << json_list(prompt)
               << ",\n  \"output_tokens\": " << json_list(tokens) << ",\n  \"text\": \"\",\n  \"load_seconds\": " << load
               << ",\n  \"first_token_seconds\": " << first << ",\n  \"generation_tokens_per_second\": " << rate
-              << ",\n  \"content_arrivals_seconds\": " << json_list(arrivals) << ",\n  \"context\": " << opt.context
+              << ",\n  \"content_arrivals_seconds\": " << json_list(arrivals)
+              << ",\n  \"matrix_seconds\": 0,\n  \"matrix_calls\": 0,\n  \"non_matrix_seconds\": 0"
+              << ",\n  \"context\": " << opt.context
               << ",\n  \"quantized_activations\": " << (opt.quantize_activations ? "true" : "false")
-              << ",\n  \"fused\": " << (opt.fused ? "true" : "false")
+              << ",\n  \"fused_ffn\": " << (opt.fused ? "true" : "false")
               << ",\n  \"token_weight_bytes\": " << info.token_weight_bytes
               << ",\n  \"hbm_roofline_fraction\": " << roofline << "\n}\n";
         }

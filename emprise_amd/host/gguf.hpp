@@ -27,7 +27,7 @@ struct MetaValue {
     bool is_array = false;
 };
 
-uint64_t encoded_bytes(WeightType type, uint64_t elements);  // gguf.cpp:72-85 (throws)
+uint64_t encoded_bytes(WeightType type, uint64_t elements);  // the reference's gguf.cpp:72-85 (throws)
 
 class Gguf {
 public:
@@ -39,6 +39,7 @@ public:
     const Tensor& tensor(const std::string& name) const;
     bool has(const std::string& name) const { return index_.count(name) != 0; }
     const MetaValue* meta(const std::string& key) const;
+    size_t metadata_count() const noexcept { return meta_.size(); }
     int meta_int(const std::string& key) const;
     float meta_float(const std::string& key) const;
     const uint8_t* data(const Tensor& t) const { return base_ + data_offset_ + t.offset; }

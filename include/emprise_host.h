@@ -20,6 +20,12 @@ extern "C" {
 
 const char* emprise_host_last_error(void);
 
+/* Gguf::Gguf (gguf.cpp:87-147) without a device: maps and validates a GGUF v2/v3 file
+ * (header, metadata, tensor table, the data section's extents) and reports how many
+ * tensors and metadata keys it holds. EMPRISE_EINVAL when the file is not a valid GGUF
+ * this reader decodes (the reference throws from the same checks). */
+emprise_status emprise_gguf_inspect(const char* path, uint64_t* tensors, uint64_t* metadata);
+
 /* ModelOptions (model.hpp:8-20) for the device path. */
 typedef struct {
     const char* path;              /* GGUF file */

@@ -67,6 +67,8 @@ def lib() -> ctypes.CDLL:
         L.eo_model_last_hidden.restype = i32
         L.eo_model_last_hidden.argtypes = [vp, _fp]
         L.eo_quantize_q8.argtypes = [_fp, sz, _fp]
+        L.eo_model_seek.restype = i32
+        L.eo_model_seek.argtypes = [vp, sz]
         L.eo_model_set_quantize_activations.argtypes = [vp, i32]
         L.eo_last_error.restype = ctypes.c_char_p
         _lib = L
@@ -214,6 +216,11 @@ class Model:
         if lib().eo_model_evaluate(self.m, token, _f(out) if logits else None):
             raise RuntimeError(lib().eo_last_error().decode())
         return out
+
+    def seek(self, position: int):
+        """Timing aid: continue at `position` with zeroed K/V rows."""
+        if lib().eo_model_seek(self.m, position):
+            raise RuntimeError(lib().eo_last_error().decode())
 
     def last_hidden(self) -> np.ndarray:
         out = np.empty(self.hidden, dtype=np.float32)

@@ -697,6 +697,24 @@ void eo_model_reset(eo_model* m) {
     }
 }
 
+/* Timing aid (no reference counterpart): moves the model to `position` as if that many
+ * positions had been evaluated, with zero K/V rows in the attention caches, so a timed
+ * decode sample runs at the positions of a long prompt (attention over position + 1
+ * rows) without evaluating the prompt. The recurrent states are left as they are. */
+int eo_model_seek(eo_model* m, size_t position) {
+    if (position >= m->context) { set_err("Context budget exhausted"); return -1; }
+    const size_t kvd = (size_t)m->kv_heads * (size_t)m->head_dim;
+    for (int l = 0; l < m->layers; ++l) {
+        eo_layer_state* S = &m->state[l];
+        if (!S->keys) continue;
+        memset(S->keys, 0, position * kvd * sizeof(float));
+        memset(S->values, 0, position * kvd * sizeof(float));
+        S->length = position;
+    }
+    m->position = position;
+    return 0;
+}
+
 static int linear(uint32_t type, const uint8_t* w, const float* x, size_t cols, float* y, size_t rows) {
     return eo_matvec(type, w, eo_encoded_bytes(type, cols * rows), x, cols, y, rows);
 }

@@ -93,6 +93,9 @@ void eo_model_reset(eo_model* m);
 void eo_model_set_quantize_activations(eo_model* m, int on);
 /* Model::Impl::evaluate (model.cpp:206-259). logits may be NULL. Returns 0 or -1. */
 int eo_model_evaluate(eo_model* m, int token, float* logits);
+/* Timing aid: jump to `position` with zeroed K/V rows (attention then spans position + 1
+ * rows, as after a prompt of that length). Returns 0 or -1. */
+int eo_model_seek(eo_model* m, size_t position);
 /* Model::generate (model.cpp:488-503) with the prompt prefilled position by position.
  * Writes up to count tokens; returns how many were emitted (EOS stops early) or -1.
  * margins (optional) gets the top-1 minus top-2 logit gap for each emitted token. */

@@ -187,3 +187,34 @@ def test_fast_q8_tiny_matches_oracle_q8(tiny_path):
     print(f"fast-q8 tiny: relative L2 to the oracle's Q8 mean {np.mean(rels):.3e} max {max(rels):.3e}; "
           f"to its FP32 path mean {np.mean(rels32):.3e}")
     assert np.mean(rels) < np.mean(rels32)
+
+
+def test_chat_cli_report(tmp_path):
+    """emprise-chat --report on the tiny model: the reference's report fields
+    (chat.cpp:77-84), valid JSON for a model path holding a quote and a backslash, and the
+    greedy tokens of the CPU oracle."""
+    import json
+    import subprocess
+    from pathlib import Path
+    exe = Path(__file__).resolve().parent.parent / "emprise_amd" / "emprise-chat"
+    d = tmp_path / 'odd "dir\\x'
+    d.mkdir()
+    model = d / "tiny.gguf"
+    synth_write(model, seed=0, **TINY)
+    prompt = synth_prompt(0, TINY["vocab"], 32)
+    report = tmp_path / "report.json"
+    r = subprocess.run([str(exe), "--model", str(model), "--prompt-ids", ",".join(map(str, prompt)), "--tokens", "16",
+                        "--context", "512", "--report", str(report)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    rep = json.loads(report.read_text())
+    want = {"engine", "backend", "model", "prompt_tokens", "output_tokens", "text", "load_seconds",
+            "first_token_seconds", "generation_tokens_per_second", "content_arrivals_seconds", "matrix_seconds",
+            "matrix_calls", "non_matrix_seconds", "context", "quantized_activations", "fused_ffn"}
+    assert want <= set(rep), want - set(rep)
+    assert rep["model"] == str(model)
+    assert rep["prompt_tokens"] == prompt and rep["context"] == 512 and rep["fused_ffn"] is True
+    assert len(rep["content_arrivals_seconds"]) == len(rep["output_tokens"]) == 16
+    assert rep["generation_tokens_per_second"] > 0
+    ref_tokens, margins = oracle.Model(str(model), context=512).generate(prompt, 16)
+    assert _greedy_agreement(rep["output_tokens"], ref_tokens, margins) >= 8
+    assert r.stdout.split() == [str(t) for t in rep["output_tokens"]]
