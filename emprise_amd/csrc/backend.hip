@@ -69,6 +69,20 @@ template <class F> void parallel_rows(uint64_t n, F f) {
     for (auto& th : pool) th.join();
 }
 
+// Upload slab size: large enough for whole rows of every shape here (a 12288-wide Q6_K row
+// is 10 KiB), small enough that copying the next slab into pinned memory overlaps the
+// DMA and re-layout of the previous one.
+constexpr uint64_t kUploadSlab = 16ull << 20;
+
+// dst <- src, n bytes, on the host threads (the source is the GGUF memory map)
+void parallel_copy(uint8_t* dst, const uint8_t* src, uint64_t n) {
+    constexpr uint64_t piece = 256 << 10;
+    parallel_rows((n + piece - 1) / piece, [&](uint64_t b, uint64_t e) {
+        const uint64_t lo = b * piece, hi = std::min(n, e * piece);
+        if (lo < hi) std::memcpy(dst + lo, src + lo, hi - lo);
+    });
+}
+
 // ---- step-program recording (emprise_hip_set_step_program) ----------------------------
 
 // An output range of a recorded phase inside a host buffer: `sel` names the phase's
@@ -111,6 +125,15 @@ static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 struct emprise_hip {
     int device = 0;
     float* noalloc_scratch = nullptr;  // this device's address of `scratch`
+    // weight upload pipeline: two pinned host slabs and two device slabs, used in turn;
+    // done[k] is recorded after slab k's copy and re-layout, so the host waits on it
+    // before filling host slab k again
+    struct Upload {
+        uint8_t* host[2] = {nullptr, nullptr};
+        uint8_t* dev[2] = {nullptr, nullptr};
+        hipEvent_t done[2] = {nullptr, nullptr};
+        uint64_t next = 0;
+    } upload;
     hipStream_t stream = nullptr;
     uint64_t budget = 0, used = 0;
     bool q8 = false;
@@ -590,6 +613,11 @@ void emprise_hip_destroy(emprise_hip* h) {
     if (h->step_err) (void)hipFree(h->step_err);
     for (auto& kv : h->weights) (void)hipFree(kv.second.dev);
     for (auto& kv : h->scratch) (void)hipFree(kv.second.ptr);
+    for (int k = 0; k < 2; ++k) {
+        if (h->upload.host[k]) (void)hipHostFree(h->upload.host[k]);
+        if (h->upload.dev[k]) (void)hipFree(h->upload.dev[k]);
+        if (h->upload.done[k]) (void)hipEventDestroy(h->upload.done[k]);
+    }
     for (auto& ev : h->events) (void)hipEventDestroy(ev);
     (void)hipStreamDestroy(h->stream);
     delete h;
@@ -662,9 +690,35 @@ emprise_status emprise_hip_upload_weight(emprise_hip* h, uint32_t type, uint64_t
     HIP_TRY(hipMalloc(&w.dev, bytes));
     const uint8_t* src = static_cast<const uint8_t*>(data);
     hipError_t err = hipSuccess;
-    if (type == kQ6K || type == kQ4K) {
-        // re-lay out in slabs of rows through a host buffer
-        const uint64_t nb = cols / 256, row_bytes = nb * type_block_bytes(type);
+    const bool blocked = type == kQ6K || type == kQ4K;
+    const uint64_t row_bytes = blocked ? cols / 256 * type_block_bytes(type) : cols * (type == kF32 ? 4 : 2);
+    // Raw GGUF bytes go through two pinned slabs in turn: the host threads copy slab i
+    // from the memory map while slab i-1's DMA and re-layout run on the stream. Block
+    // encodings are re-laid out on the device (launch_repack), whole rows per slab.
+    if (row_bytes <= kUploadSlab) {
+        auto& up = h->upload;
+        for (int k = 0; k < 2 && err == hipSuccess; ++k) {
+            if (!up.host[k]) err = hipHostMalloc(reinterpret_cast<void**>(&up.host[k]), kUploadSlab, hipHostMallocDefault);
+            if (err == hipSuccess && !up.dev[k]) err = hipMalloc(&up.dev[k], kUploadSlab);
+            if (err == hipSuccess && !up.done[k]) err = hipEventCreateWithFlags(&up.done[k], hipEventDisableTiming);
+        }
+        const uint64_t slab_rows = kUploadSlab / row_bytes;
+        for (uint64_t r0 = 0; r0 < rows && err == hipSuccess; r0 += slab_rows) {
+            const uint64_t n = std::min(slab_rows, rows - r0), nbytes = n * row_bytes;
+            const int k = (int)(up.next++ & 1);
+            err = hipEventSynchronize(up.done[k]);
+            if (err != hipSuccess) break;
+            parallel_copy(up.host[k], src + r0 * row_bytes, nbytes);
+            if (blocked) {
+                err = hipMemcpyAsync(up.dev[k], up.host[k], nbytes, hipMemcpyHostToDevice, h->stream);
+                if (err == hipSuccess) err = launch_repack(type, up.dev[k], w.dev + r0 * row_bytes, n, cols, h->stream);
+            } else {
+                err = hipMemcpyAsync(w.dev + r0 * row_bytes, up.host[k], nbytes, hipMemcpyHostToDevice, h->stream);
+            }
+            if (err == hipSuccess) err = hipEventRecord(up.done[k], h->stream);
+        }
+    } else if (blocked) {
+        // rows wider than a slab (not met by qwen35 shapes): re-laid out on the host
         const uint64_t slab_rows = std::max<uint64_t>(1, (64ull << 20) / row_bytes);
         std::vector<uint8_t> buf((size_t)(std::min(rows, slab_rows) * row_bytes));
         for (uint64_t r0 = 0; r0 < rows && err == hipSuccess; r0 += slab_rows) {
@@ -680,6 +734,7 @@ emprise_status emprise_hip_upload_weight(emprise_hip* h, uint32_t type, uint64_t
         err = hipMemcpy(w.dev, src, bytes, hipMemcpyHostToDevice);
     }
     if (err != hipSuccess) {
+        (void)hipStreamSynchronize(h->stream);
         (void)hipFree(w.dev);
         return fail(EMPRISE_EDEVICE, "upload weights: %s", hipGetErrorString(err));
     }

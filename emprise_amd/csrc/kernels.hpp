@@ -77,6 +77,9 @@ size_t matvec_lds_bytes(uint32_t type, int cols, bool q8);
 int matvec_rows_per_group(uint32_t type, uint64_t cols, int mode, uint64_t total_rows);
 hipError_t launch_matvec(uint32_t type, bool q8, const MvArgs& a, int grid_cap, hipStream_t stream);
 hipError_t launch_matvec_stream(uint32_t type, bool q8, const MvArgs& a, hipStream_t stream);
+// Raw GGUF Q6_K / Q4_K rows (device) -> the kernel layout of layout.hpp (device).
+hipError_t launch_repack(uint32_t type, const uint8_t* src, uint8_t* dst, uint64_t rows, uint64_t cols,
+                         hipStream_t stream);
 hipError_t launch_dequant_rows(const uint8_t* w, uint32_t type, int cols, uint64_t row0, uint64_t n, float* out,
                                hipStream_t stream);
 
