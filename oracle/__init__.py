@@ -62,6 +62,8 @@ def lib() -> ctypes.CDLL:
         L.eo_model_reset.argtypes = [vp]
         L.eo_model_evaluate.restype = i32
         L.eo_model_evaluate.argtypes = [vp, i32, _fp]
+        L.eo_model_evaluate_many.restype = i32
+        L.eo_model_evaluate_many.argtypes = [vp, ctypes.POINTER(ctypes.c_int), sz, _fp]
         L.eo_model_generate.restype = i32
         L.eo_model_generate.argtypes = [vp, ctypes.POINTER(ctypes.c_int), sz, sz, ctypes.POINTER(ctypes.c_int), _fp]
         L.eo_model_last_hidden.restype = i32
@@ -214,6 +216,15 @@ class Model:
     def evaluate(self, token: int, logits: bool = True):
         out = np.empty(self.vocab, dtype=np.float32) if logits else None
         if lib().eo_model_evaluate(self.m, token, _f(out) if logits else None):
+            raise RuntimeError(lib().eo_last_error().decode())
+        return out
+
+    def evaluate_many(self, tokens, logits: bool = True):
+        """len(tokens) positions at once, with the bits of that many evaluate() calls;
+        the logits are the last position's."""
+        out = np.empty(self.vocab, dtype=np.float32) if logits else None
+        t = (ctypes.c_int * len(tokens))(*tokens)
+        if lib().eo_model_evaluate_many(self.m, t, len(tokens), _f(out) if logits else None):
             raise RuntimeError(lib().eo_last_error().decode())
         return out
 

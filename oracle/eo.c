@@ -815,6 +815,143 @@ int eo_model_evaluate(eo_model* m, int token, float* logits) {
     return rc;
 }
 
+/* Projections of n positions at once: Y[p * rows + r] = row r of the matrix times
+ * X[p * cols ...], each output the same single FP32 sum in element order as eo_matvec
+ * (no fused multiply-add: -ffp-contract=off), so every value equals eo_matvec's bit for
+ * bit. Positions advance together in tiles of EO_TILE: a weight block is decoded once
+ * per tile, and the tile's sums are independent lanes the compiler can vectorise. */
+#define EO_TILE 64
+static int matmul_rows(uint32_t type, const uint8_t* w, const float* X, size_t n, size_t cols, float* Y,
+                       size_t rows) {
+    const uint64_t row_bytes = eo_encoded_bytes(type, cols);
+    if (!cols || !row_bytes) { set_err("Matrix size mismatch"); return -1; }
+    float* xt = (float*)malloc(cols * EO_TILE * sizeof(float));
+    if (!xt) { set_err("Out of memory"); return -1; }
+    const size_t es = type == EO_F32 ? 4 : 2;
+    for (size_t p0 = 0; p0 < n; p0 += EO_TILE) {
+        const size_t t = n - p0 < EO_TILE ? n - p0 : EO_TILE;
+        for (size_t c = 0; c < cols; ++c)
+            for (size_t q = 0; q < EO_TILE; ++q) xt[c * EO_TILE + q] = q < t ? X[(p0 + q) * cols + c] : 0.f;
+        #pragma omp parallel for schedule(static)
+        for (int64_t row = 0; row < (int64_t)rows; ++row) {
+            const uint8_t* ptr = w + (uint64_t)row * row_bytes;
+            float sum[EO_TILE];
+            float block[256];
+            for (int q = 0; q < EO_TILE; ++q) sum[q] = 0.f;
+            for (size_t k = 0; k < cols; k += 256) {
+                const size_t len = cols - k < 256 ? cols - k : 256;
+                if (type == EO_Q6_K) q6_block(ptr + k / 256 * 210, block);
+                else if (type == EO_Q4_K) q4_k_block(ptr + k / 256 * 144, block);
+                else for (size_t j = 0; j < len; ++j) block[j] = raw_element(type, ptr + (k + j) * es);
+                for (size_t j = 0; j < len; ++j) {
+                    const float wj = block[j];
+                    const float* xr = xt + (k + j) * EO_TILE;
+                    for (int q = 0; q < EO_TILE; ++q) sum[q] += wj * xr[q];
+                }
+            }
+            for (size_t q = 0; q < t; ++q) Y[(p0 + q) * rows + (size_t)row] = sum[q];
+        }
+    }
+    free(xt);
+    return 0;
+}
+
+/* matmul_rows with mlinear's --fast-q8 rule applied to each position's input. */
+static int model_matmul(const eo_model* m, uint32_t type, const uint8_t* w, const float* X, size_t n, size_t cols,
+                        float* Y, size_t rows) {
+    if (!m->q8 || type != EO_Q6_K) return matmul_rows(type, w, X, n, cols, Y, rows);
+    float* xq = (float*)malloc(n * cols * sizeof(float));
+    if (!xq) { set_err("Out of memory"); return -1; }
+    for (size_t p = 0; p < n; ++p) eo_quantize_q8(X + p * cols, cols, xq + p * cols);
+    const int rc = matmul_rows(type, w, xq, n, cols, Y, rows);
+    free(xq);
+    return rc;
+}
+
+/* n positions from the current one, with the same bits as n calls of eo_model_evaluate
+ * (the reference's chunked prefill, model.cpp:355-366, whose CPU-backend projections are
+ * per-position loops, backend.cpp:81-90): every projection of the n positions runs as
+ * one matmul_rows, the recurrent and attention steps run position by position in order.
+ * logits (optional) are the last position's. Test and fixture generation aid. */
+int eo_model_evaluate_many(eo_model* m, const int* tokens, size_t n, float* logits) {
+    if (!n) { set_err("Empty token list"); return -1; }
+    if (m->position >= m->context || n > m->context - m->position) { set_err("Context budget exhausted"); return -1; }
+    for (size_t p = 0; p < n; ++p)
+        if (tokens[p] < 0 || tokens[p] >= m->vocab) { set_err("Token ID"); return -1; }
+    const size_t H = (size_t)m->hidden, F = (size_t)m->ffn, vh = (size_t)m->value_heads;
+    const size_t kd = (size_t)m->key_heads * m->state_dim, vd = vh * m->state_dim, ch = 2 * kd + vd;
+    const size_t qd = (size_t)m->heads * m->head_dim * 2, kvd = (size_t)m->kv_heads * m->head_dim;
+    const size_t ad = (size_t)m->heads * m->head_dim;
+    const size_t w0 = ch > qd ? ch : qd, w1 = vd > kvd ? vd : kvd, w2 = vh > kvd ? vh : kvd, w4 = vd > ad ? vd : ad;
+    const size_t row_bytes = eo_encoded_bytes(m->tembd, H);
+    float* x = (float*)malloc(n * H * sizeof(float));
+    float* nrm = (float*)malloc(n * H * sizeof(float));
+    float* attn = (float*)malloc(n * H * sizeof(float));
+    float* b0 = (float*)malloc(n * w0 * sizeof(float));
+    float* b1 = (float*)malloc(n * w1 * sizeof(float));
+    float* b2 = (float*)malloc(n * w2 * sizeof(float));
+    float* b3 = (float*)malloc(n * vh * sizeof(float));
+    float* b4 = (float*)malloc(n * w4 * sizeof(float));
+    float* g = (float*)malloc(n * F * sizeof(float));
+    float* u = (float*)malloc(n * F * sizeof(float));
+    int rc = 0;
+    if (!x || !nrm || !attn || !b0 || !b1 || !b2 || !b3 || !b4 || !g || !u) { set_err("Out of memory"); rc = -1; }
+    for (size_t p = 0; rc == 0 && p < n; ++p)
+        rc = eo_dequantize(m->tembd, m->embd + (size_t)tokens[p] * row_bytes, row_bytes, x + p * H, H);
+    for (int l = 0; rc == 0 && l < m->layers; ++l) {
+        eo_layer* L = &m->layer[l];
+        eo_layer_state* S = &m->state[l];
+        memcpy(nrm, x, n * H * sizeof(float));
+        for (size_t p = 0; p < n; ++p) eo_rms(nrm + p * H, H, L->attn_norm, m->eps);
+        if (L->recurrent) {
+            if ((rc = model_matmul(m, L->tqkv, L->qkv, nrm, n, H, b0, ch))) break;
+            if ((rc = model_matmul(m, L->tgate, L->gate, nrm, n, H, b1, vd))) break;
+            if ((rc = model_matmul(m, L->talpha, L->alpha, nrm, n, H, b2, vh))) break;
+            if ((rc = model_matmul(m, L->tbeta, L->beta, nrm, n, H, b3, vh))) break;
+            for (size_t p = 0; p < n; ++p)
+                eo_delta_net(m->key_heads, m->value_heads, m->state_dim, m->conv_width, m->eps, b0 + p * ch,
+                             b1 + p * vd, b2 + p * vh, b3 + p * vh, L->conv, L->ssm_a, L->dt, L->ssm_norm, S->conv,
+                             S->rec, b4 + p * vd);
+            if ((rc = model_matmul(m, L->tout, L->out, b4, n, vd, attn, H))) break;
+        } else {
+            if ((rc = model_matmul(m, L->tq, L->q, nrm, n, H, b0, qd))) break;
+            if ((rc = model_matmul(m, L->tk, L->k, nrm, n, H, b1, kvd))) break;
+            if ((rc = model_matmul(m, L->tv, L->v, nrm, n, H, b2, kvd))) break;
+            for (size_t p = 0; p < n; ++p) {
+                S->length += 1;
+                eo_attention(m->heads, m->kv_heads, m->head_dim, m->rotary, m->rope_base, m->eps, L->q_norm,
+                             L->k_norm, b0 + p * qd, b1 + p * kvd, b2 + p * kvd, S->keys, S->values, S->length,
+                             (int)(m->position + p), b4 + p * ad);
+            }
+            if ((rc = model_matmul(m, L->to, L->o, b4, n, ad, attn, H))) break;
+        }
+        for (size_t i = 0; i < n * H; ++i) x[i] += attn[i];
+        memcpy(nrm, x, n * H * sizeof(float));
+        for (size_t p = 0; p < n; ++p) eo_rms(nrm + p * H, H, L->post_norm, m->eps);
+        /* model_feed_forward / eo_feed_forward over the n positions */
+        if ((rc = model_matmul(m, L->tfg, L->fg, nrm, n, H, g, F))) break;
+        if ((rc = model_matmul(m, L->tfu, L->fu, nrm, n, H, u, F))) break;
+        for (size_t i = 0; i < n * F; ++i) {
+            const float e = expf(-fabsf(g[i]));
+            const float s = g[i] >= 0 ? 1.f / (1.f + e) : e / (1.f + e);
+            g[i] = g[i] * s * u[i];
+        }
+        if ((rc = model_matmul(m, L->tfd, L->fd, g, n, F, attn, H))) break;
+        for (size_t i = 0; i < n * H; ++i) x[i] += attn[i];
+    }
+    if (rc == 0) {
+        float* last = x + (n - 1) * H;
+        memcpy(m->last_hidden, last, H * sizeof(float));
+        if (logits) {
+            eo_rms(last, H, m->output_norm, m->eps);
+            rc = mlinear(m, m->toutput, m->output, last, H, logits, (size_t)m->vocab);
+        }
+        if (rc == 0) m->position += n;
+    }
+    free(x); free(nrm); free(attn); free(b0); free(b1); free(b2); free(b3); free(b4); free(g); free(u);
+    return rc;
+}
+
 int eo_model_last_hidden(const eo_model* m, float* out) {
     memcpy(out, m->last_hidden, (size_t)m->hidden * sizeof(float));
     return 0;

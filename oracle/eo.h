@@ -93,6 +93,10 @@ void eo_model_reset(eo_model* m);
 void eo_model_set_quantize_activations(eo_model* m, int on);
 /* Model::Impl::evaluate (model.cpp:206-259). logits may be NULL. Returns 0 or -1. */
 int eo_model_evaluate(eo_model* m, int token, float* logits);
+/* tokens[0..n) from the current position, bit for bit as n eo_model_evaluate calls, with
+ * the projections of all n positions computed together (one weight decode per 64
+ * positions). logits (optional) are the last position's. Returns 0 or -1. */
+int eo_model_evaluate_many(eo_model* m, const int* tokens, size_t n, float* logits);
 /* Timing aid: jump to `position` with zeroed K/V rows (attention then spans position + 1
  * rows, as after a prompt of that length). Returns 0 or -1. */
 int eo_model_seek(eo_model* m, size_t position);

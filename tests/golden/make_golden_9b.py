@@ -21,7 +21,7 @@ Outputs (tests/golden/):
   c4b_9b_q4km_q8.npz   logits after the last prompt position
 
 Usage: python tests/golden/make_golden_9b.py [c4b] [c3] [c4a]   (all by default)
-Runs for roughly an hour on 8 cores (the C4a prompt is 2048 positions).
+Runs for roughly half an hour on 8 cores.
 """
 import hashlib
 import json
@@ -73,14 +73,16 @@ def top2(logits):
 
 
 def run(path: Path, prompt, count: int, fast_q8: bool):
-    """Greedy decode as Model::generate (model.cpp:488-503), position by position."""
+    """Greedy decode as Model::generate (model.cpp:488-503): the prompt through
+    evaluate_many (the bits of position-by-position evaluation, pinned in
+    tests/test_golden.py), then one position per token."""
     m = oracle.Model(str(path), context=CONTEXT, threads=os.cpu_count() or 1, fast_q8=fast_q8)
     t0 = time.time()
     logits = None
-    for i, t in enumerate(prompt):
-        logits = m.evaluate(t, logits=(i + 1 == len(prompt)))
-        if (i + 1) % 128 == 0:
-            print(f"  prompt {i + 1}/{len(prompt)} ({time.time() - t0:.0f}s)", flush=True)
+    for start in range(0, len(prompt), 256):
+        chunk = prompt[start:start + 256]
+        logits = m.evaluate_many(chunk, logits=(start + len(chunk) == len(prompt)))
+        print(f"  prompt {start + len(chunk)}/{len(prompt)} ({time.time() - t0:.0f}s)", flush=True)
     prompt_logits = logits.copy()
     tokens, margins, v1s, v2s = [], [], [], []
     for i in range(count):

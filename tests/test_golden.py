@@ -37,3 +37,29 @@ def test_tiny_model_tokens_match_reference_composition(tmp_path):
     tokens, margins = m.generate(g["prompt"], len(g["tokens"]))
     assert tokens == g["tokens"]
     assert np.allclose(margins, g["margins"], rtol=0, atol=0)
+
+
+def test_evaluate_many_has_the_bits_of_single_positions(tmp_path):
+    """The batched prompt evaluation that writes the 9B fixtures (eo_model_evaluate_many)
+    against the position-by-position evaluate pinned above: logits, the last residual and
+    the state it leaves (the next position's logits) all bit for bit, across a 64-position
+    tile boundary, from position 0 and from a later position, plain and with --fast-q8,
+    on the all-Q6_K and the Q4_K_M-mix tiny models."""
+    from emprise_amd import TINY, synth_prompt, synth_write
+    prompt = synth_prompt(5, TINY["vocab"], 75)
+    for mix in (False, True):
+        p = tmp_path / f"tiny_{mix}.gguf"
+        synth_write(p, seed=3, q4_k_m_mix=mix, **TINY)
+        for q8 in (False, True):
+            ref = oracle.Model(str(p), context=128, fast_q8=q8)
+            many = oracle.Model(str(p), context=128, fast_q8=q8)
+            for start, stop in ((0, 1), (1, 70), (70, 75)):
+                for t in prompt[start:stop]:
+                    want = ref.evaluate(t)
+                got = many.evaluate_many(prompt[start:stop])
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (mix, q8, start)
+                assert np.array_equal(many.last_hidden().view(np.uint32), ref.last_hidden().view(np.uint32))
+            nxt = prompt[0]
+            assert np.array_equal(many.evaluate(nxt).view(np.uint32), ref.evaluate(nxt).view(np.uint32))
+            ref.close()
+            many.close()
