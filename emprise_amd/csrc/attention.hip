@@ -120,6 +120,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     ldv<E>(qn, a.q_norm + E * lane);
     ldv<E>(kn, a.k_norm + E * lane);
     const float vin_d = vin[min((int)threadIdx.x, HD - 1)];
+    // this thread's first RoPE pair (idx = threadIdx.x below): its (cos, sin) from the table
+    const int half = a.rotary / 2;
+    const float2 cs0 = half > 0 ? a.rope[(size_t)pos * half + min((int)threadIdx.x, (group + 1) * half - 1) % half]
+                                : make_float2(1.f, 0.f);
     float kr[PW][E], vr[PW][E];
     load_rows(kr, vr, sub0);
 
@@ -141,13 +145,14 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     }
     if (threadIdx.x < HD) vnew[threadIdx.x] = vin_d;
     lds_barrier();
-    // NEOX RoPE over the first `rotary` dims (model.cpp:121-127); one thread per pair.
-    const int half = a.rotary / 2;
+    // NEOX RoPE over the first `rotary` dims (model.cpp:121-127); one thread per pair,
+    // the angles' cos and sin from the backend's table (rope_table_kernel), which the
+    // step program and the batched prefill read as well
     for (int idx = threadIdx.x; idx < (group + 1) * half; idx += blockDim.x) {
         const int g = idx / half, i = idx % half;
         float* row = g < group ? qs[g] : knew;
-        const float angle = (float)pos / powf(a.rope_base, 2.f * (float)i / (float)a.rotary);
-        const float c = cosf(angle), s = sinf(angle);
+        const float2 cs = idx == (int)threadIdx.x ? cs0 : a.rope[(size_t)pos * half + i];
+        const float c = cs.x, s = cs.y;
         const float x0 = row[i], x1 = row[i + half];
         row[i] = x0 * c - x1 * s;
         row[i + half] = x0 * s + x1 * c;
@@ -338,6 +343,18 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
     }
 }
 
+// (cos, sin) of angle = pos / base^(2i / rotary) for every position < context and
+// i < rotary / 2 (model.cpp:121-127), with the expressions attention_kernel used inline.
+__global__ __launch_bounds__(256) void rope_table_kernel(float2* t, int context, int rotary, float base) {
+    const int half = rotary / 2;
+    const size_t n = (size_t)context * half;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (size_t)gridDim.x * blockDim.x) {
+        const int pos = (int)(idx / half), i = (int)(idx % half);
+        const float angle = (float)pos / powf(base, 2.f * (float)i / (float)rotary);
+        t[idx] = make_float2(cosf(angle), sinf(angle));
+    }
+}
+
 // ---- batched form: `count` consecutive prompt positions (the prefill) --------------------
 //
 // Position t (absolute p0 + t) attends over 0..p0+t. The dense parts run on the matrix
@@ -378,8 +395,8 @@ __global__ __launch_bounds__(512) void attn_prep_batch_kernel(AttnBatchArgs a) {
     for (int idx = threadIdx.x; idx < nh * half; idx += blockDim.x) {
         const int v = idx / half, i = idx % half;
         float* r = rows + (size_t)v * HD;
-        const float angle = (float)pos / powf(a.rope_base, 2.f * (float)i / (float)a.rotary);
-        const float c = cosf(angle), s = sinf(angle);
+        const float2 cs = a.rope[(size_t)pos * half + i];
+        const float c = cs.x, s = cs.y;
         const float x0 = r[i], x1 = r[i + half];
         r[i] = x0 * c - x1 * s;
         r[i + half] = x0 * s + x1 * c;
@@ -477,6 +494,14 @@ hipError_t launch_attention_batch(const AttnBatchArgs& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     const size_t n = (size_t)a.count * a.heads * hd;
     launch_kernel(attn_gate_batch_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_table(float2* table, int context, int rotary, float base, hipStream_t stream) {
+    const size_t n = (size_t)context * (rotary / 2);
+    if (!n) return hipSuccess;
+    launch_kernel(rope_table_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0, stream,
+                  table, context, rotary, base);
     return hipGetLastError();
 }
 

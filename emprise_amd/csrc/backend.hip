@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <set>
 #include <string>
 #include <thread>
 #include <unordered_map>
@@ -150,6 +151,7 @@ struct emprise_hip {
         size_t bytes = 0;
     };
     std::unordered_map<std::string, Scratch> scratch;
+    std::set<std::string> rope_ready;  // RoPE tables (scratch keys) already filled
     // kernel trace (emprise_hip_trace_begin/end)
     struct TraceRec {
         const char* kernel;
@@ -1216,6 +1218,27 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
     return run_matvec(h, &po, 1, kMvPlain, nullptr, dn, nullptr, nullptr, 0, nullptr);
 }
 
+namespace {
+// The RoPE table (cos, sin of every position's angles) of this (context, rotary, base),
+// shared by the decode, step-program and prefill attention so that they rotate with the
+// same values; filled by the first eager call (not while a graph is being captured).
+emprise_status rope_table(emprise_hip* h, const emprise_hip_attention_params* p, const float2** out) {
+    uint32_t bits;
+    std::memcpy(&bits, &p->rope_base, 4);
+    char key[96];
+    std::snprintf(key, sizeof key, "rope:%d:%d:%08x", p->context, p->rotary, bits);
+    void* t;
+    TRY(h->get_scratch(key, std::max<size_t>((size_t)p->context * (p->rotary / 2) * sizeof(float2), 8), &t));
+    if (!h->rope_ready.count(key)) {
+        if (h->capturing) return fail(EMPRISE_ESTATE, "the RoPE table must be filled before graph capture");
+        TRY(launched(launch_rope_table(static_cast<float2*>(t), p->context, p->rotary, p->rope_base, h->stream)));
+        h->rope_ready.insert(key);
+    }
+    *out = static_cast<const float2*>(t);
+    return EMPRISE_OK;
+}
+}  // namespace
+
 emprise_status emprise_hip_attention_batch(emprise_hip* h, const emprise_hip_attention_params* p, emprise_dev qkv,
                                            int count, uint64_t stride, int first_position, emprise_dev out,
                                            uint64_t out_stride) {
@@ -1233,6 +1256,7 @@ emprise_status emprise_hip_attention_batch(emprise_hip* h, const emprise_hip_att
                     first_position, first_position + count - 1, p->context, (unsigned long long)stride);
     if (h->recording) return rec_unsupported(h, "batched attention");
     AttnBatchArgs a{};
+    TRY(rope_table(h, p, &a.rope));
     a.heads = p->heads;
     a.kv_heads = p->kv_heads;
     a.head_dim = p->head_dim;
@@ -1293,6 +1317,7 @@ emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention
     a.position = reinterpret_cast<const int*>(p->position);
     a.out = reinterpret_cast<float*>(out);
     a.partial = static_cast<float*>(partial);
+    TRY(rope_table(h, p, &a.rope));
     if (h->recording) {
         const int chunks = (p->context + kAttnChunk - 1) / kAttnChunk;
         if ((p->head_dim != 128 && p->head_dim != 256) || chunks > 1024)
@@ -1309,6 +1334,7 @@ emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention
         sa.context = a.context;
         sa.eps = a.eps;
         sa.rope_base = a.rope_base;
+        sa.rope = a.rope;
         sa.q_norm = a.q_norm;
         sa.k_norm = a.k_norm;
         sa.keys = a.keys;

@@ -156,6 +156,7 @@ struct AttnArgs {
     const int* position;
     float* out;
     float* partial;  // scratch: [kv_heads][chunks][group][head_dim + 2]
+    const float2* rope;  // [context][rotary / 2]: (cos, sin) of pos / base^(2i / rotary)
 };
 constexpr int kAttnChunk = 64;    // positions per partial of the step program's attention
 constexpr int kAttnSub = 16;     // positions per step of attention_kernel's online softmax
@@ -167,6 +168,7 @@ constexpr int kAttnSplit = 64;   // position ranges (workgroups) per KV head of 
 struct AttnBatchArgs {
     int heads, kv_heads, head_dim, rotary, count, first, lp;
     float eps, rope_base;
+    const float2* rope;  // [context][rotary / 2] (cos, sin), as AttnArgs::rope
     const float* q_norm;
     const float* k_norm;
     const float* qkv;
@@ -183,6 +185,8 @@ struct AttnBatchArgs {
 hipError_t launch_attention_batch(const AttnBatchArgs& a, hipStream_t stream);
 size_t attention_partial_floats(int heads, int kv_heads, int head_dim, int context);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+// The RoPE table of attention_kernel: (cos, sin) of every position's angles.
+hipError_t launch_rope_table(float2* table, int context, int rotary, float base, hipStream_t stream);
 
 // ---- small ops ----
 hipError_t launch_fill(float* dst, float value, size_t n, hipStream_t stream);

@@ -633,8 +633,8 @@ __device__ void step_attention(const StepAttention& a, uint32_t tag, uint32_t ba
         for (int idx = threadIdx.x; idx < (group + 1) * half; idx += blockDim.x) {
             const int gg = idx / half, i = idx % half;
             float* row = gg < group ? qs[gg] : knew;
-            const float angle = (float)pos / powf(a.rope_base, 2.f * (float)i / (float)a.rotary);
-            const float c = cosf(angle), s = sinf(angle);
+            const float* cs = reinterpret_cast<const float*>(a.rope) + 2 * ((size_t)pos * half + i);
+            const float c = gc(cs)[0], s = gc(cs)[1];
             const float x0 = row[i], x1 = row[i + half];
             row[i] = x0 * c - x1 * s;
             row[i + half] = x0 * s + x1 * c;

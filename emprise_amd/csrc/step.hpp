@@ -80,6 +80,7 @@ struct StepGdn {
 struct StepAttention {
     int heads, kv_heads, head_dim, rotary, context;
     float eps, rope_base;
+    const float2* rope;  // [context][rotary / 2] (cos, sin)
     const float* q_norm;
     const float* k_norm;
     StepIn qkv;        // [q+gate interleaved per head | k | v]

@@ -374,7 +374,7 @@ def _attention_case(backend, heads, kv, hd, rot, L, context, seed, base=1e7, eps
         backend.free(b)
 
 
-@pytest.mark.parametrize("L", [1, 2, 63, 64, 65, 512, 2048, 4096])
+@pytest.mark.parametrize("L", [1, 2, 63, 64, 65, 129, 512, 1025, 2048, 4095, 4096])
 def test_attention_config2b(backend, L):
     """Config 2b: 16 Q / 4 KV heads, head_dim 256, partial RoPE over 64 dims."""
     _attention_case(backend, 16, 4, 256, 64, L, 4096, seed=L)
