@@ -150,7 +150,8 @@ class AttentionParams(ctypes.Structure):
     _fields_ = [("heads", ctypes.c_int), ("kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
                 ("rotary", ctypes.c_int), ("context", ctypes.c_int), ("eps", ctypes.c_float),
                 ("rope_base", ctypes.c_float), ("q_norm", ctypes.c_uint64), ("k_norm", ctypes.c_uint64),
-                ("keys", ctypes.c_uint64), ("values", ctypes.c_uint64), ("position", ctypes.c_uint64)]
+                ("keys", ctypes.c_uint64), ("values", ctypes.c_uint64), ("position", ctypes.c_uint64),
+                ("rope_position", ctypes.c_uint64)]
 
 
 class HipBackend:
@@ -404,7 +405,7 @@ class SynthConfig(ctypes.Structure):
                 ("value_heads", ctypes.c_int), ("state_dim", ctypes.c_int), ("conv_width", ctypes.c_int),
                 ("full_attention_interval", ctypes.c_int), ("context_length", ctypes.c_int),
                 ("rope_base", ctypes.c_float), ("eps", ctypes.c_float), ("eos", ctypes.c_int),
-                ("matrix_type", ctypes.c_uint32), ("q4_k_m_mix", ctypes.c_int)]
+                ("matrix_type", ctypes.c_uint32), ("q4_k_m_mix", ctypes.c_int), ("mtp", ctypes.c_int)]
 
 
 # The benchmark's model shapes. TINY is config 0 (hidden 512, 4 layers GDN,GDN,GDN,attention,
@@ -448,6 +449,18 @@ def host_lib() -> ctypes.CDLL:
     lib.emprise_model_evaluate.argtypes = [vp, ctypes.c_int, P(ctypes.c_float)]
     lib.emprise_model_last_hidden.restype = ctypes.c_int
     lib.emprise_model_last_hidden.argtypes = [vp, P(ctypes.c_float)]
+    lib.emprise_model_last_hidden_normed.restype = ctypes.c_int
+    lib.emprise_model_last_hidden_normed.argtypes = [vp, P(ctypes.c_float)]
+    lib.emprise_model_evaluate_block.restype = ctypes.c_int
+    lib.emprise_model_evaluate_block.argtypes = [vp, P(ctypes.c_int), ctypes.c_size_t, P(ctypes.c_float)]
+    lib.emprise_model_has_mtp.restype = ctypes.c_int
+    lib.emprise_model_has_mtp.argtypes = [vp]
+    lib.emprise_model_mtp_draft.restype = ctypes.c_int
+    lib.emprise_model_mtp_draft.argtypes = [vp, P(ctypes.c_float), ctypes.c_int, ctypes.c_size_t, P(ctypes.c_float)]
+    lib.emprise_model_mtp_hidden.restype = ctypes.c_int
+    lib.emprise_model_mtp_hidden.argtypes = [vp, P(ctypes.c_float)]
+    lib.emprise_model_reset_mtp.restype = ctypes.c_int
+    lib.emprise_model_reset_mtp.argtypes = [vp]
     lib.emprise_gguf_inspect.restype = ctypes.c_int
     lib.emprise_gguf_inspect.argtypes = [ctypes.c_char_p, P(ctypes.c_uint64), P(ctypes.c_uint64)]
     lib.emprise_model_prefill.restype = ctypes.c_int
@@ -465,6 +478,10 @@ def host_lib() -> ctypes.CDLL:
     return lib
 
 
+def _fptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
 def _host_check(status: int):
     if status != OK:
         msg = host_lib().emprise_host_last_error().decode()
@@ -473,9 +490,10 @@ def _host_check(status: int):
         raise EmpriseError(status, msg)
 
 
-def synth_write(path, seed: int = 0, matrix_type: int = Q6_K, q4_k_m_mix: bool = False, **shape):
-    """Writes a deterministic synthetic qwen35 GGUF (see emprise_synth_write)."""
-    c = SynthConfig(seed=seed, matrix_type=matrix_type, q4_k_m_mix=int(q4_k_m_mix), **shape)
+def synth_write(path, seed: int = 0, matrix_type: int = Q6_K, q4_k_m_mix: bool = False, mtp: bool = False, **shape):
+    """Writes a deterministic synthetic qwen35 GGUF (see emprise_synth_write); mtp adds the
+    next-n block blk.<layers>."""
+    c = SynthConfig(seed=seed, matrix_type=matrix_type, q4_k_m_mix=int(q4_k_m_mix), mtp=int(mtp), **shape)
     _host_check(host_lib().emprise_synth_write(ctypes.byref(c), str(path).encode()))
 
 
@@ -549,10 +567,42 @@ class Model:
         _host_check(host_lib().emprise_model_prefill(self.m, p, len(tokens), ptr))
         return out
 
-    def last_hidden(self) -> np.ndarray:
+    def last_hidden(self, normed: bool = False) -> np.ndarray:
+        """The residual after the last position with logits (Model::last_hidden_raw), or
+        with normed=True that residual through the output norm (Model::last_hidden)."""
         out = np.empty(self.info.hidden, dtype=np.float32)
-        _host_check(host_lib().emprise_model_last_hidden(self.m, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        fn = host_lib().emprise_model_last_hidden_normed if normed else host_lib().emprise_model_last_hidden
+        _host_check(fn(self.m, _fptr(out)))
         return out
+
+    def evaluate_block(self, tokens) -> np.ndarray:
+        """Model::evaluate_block: the tokens from the current position on, every
+        position's logits (len(tokens) x vocab)."""
+        p = (ctypes.c_int * len(tokens))(*tokens)
+        out = np.empty((len(tokens), self.info.vocab), dtype=np.float32)
+        _host_check(host_lib().emprise_model_evaluate_block(self.m, p, len(tokens), _fptr(out)))
+        return out
+
+    @property
+    def has_mtp(self) -> bool:
+        return bool(host_lib().emprise_model_has_mtp(self.m))
+
+    def mtp_draft(self, hidden, token: int, position: int) -> np.ndarray:
+        """Model::mtp_draft: the MTP head's logits for the token after `token`."""
+        h = np.ascontiguousarray(hidden, dtype=np.float32)
+        if h.shape != (self.info.hidden,):
+            raise ValueError(f"hidden must have {self.info.hidden} floats")
+        out = np.empty(self.info.vocab, dtype=np.float32)
+        _host_check(host_lib().emprise_model_mtp_draft(self.m, _fptr(h), token, position, _fptr(out)))
+        return out
+
+    def mtp_hidden(self) -> np.ndarray:
+        out = np.empty(self.info.hidden, dtype=np.float32)
+        _host_check(host_lib().emprise_model_mtp_hidden(self.m, _fptr(out)))
+        return out
+
+    def reset_mtp(self):
+        _host_check(host_lib().emprise_model_reset_mtp(self.m))
 
     def trace_step(self, token: int):
         """One eager step with per-launch HIP event timing: [(kernel, bytes, ms), ...]."""

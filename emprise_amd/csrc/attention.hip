@@ -79,6 +79,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     const int kvh = blockIdx.x / kAttnSplit, range = blockIdx.x % kAttnSplit;
     const int pos = *a.position;
     if (pos < 0 || pos >= a.context) return;  // the host keeps positions inside the caches
+    const int rpos = a.rope_position ? *a.rope_position : pos;
+    if (rpos < 0 || rpos >= a.context) return;  // the RoPE table has `context` rows
     const int len = pos + 1;
     const int nsub = (len + CH - 1) / CH, per = attn_per(len);
     const int sub0 = range * per, sub1 = min(nsub, sub0 + per);
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     const float vin_d = vin[min((int)threadIdx.x, HD - 1)];
     // this thread's first RoPE pair (idx = threadIdx.x below): its (cos, sin) from the table
     const int half = a.rotary / 2;
-    const float2 cs0 = half > 0 ? a.rope[(size_t)pos * half + min((int)threadIdx.x, (group + 1) * half - 1) % half]
+    const float2 cs0 = half > 0 ? a.rope[(size_t)rpos * half + min((int)threadIdx.x, (group + 1) * half - 1) % half]
                                 : make_float2(1.f, 0.f);
     float kr[PW][E], vr[PW][E];
     load_rows(kr, vr, sub0);
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     for (int idx = threadIdx.x; idx < (group + 1) * half; idx += blockDim.x) {
         const int g = idx / half, i = idx % half;
         float* row = g < group ? qs[g] : knew;
-        const float2 cs = idx == (int)threadIdx.x ? cs0 : a.rope[(size_t)pos * half + i];
+        const float2 cs = idx == (int)threadIdx.x ? cs0 : a.rope[(size_t)rpos * half + i];
         const float c = cs.x, s = cs.y;
         const float x0 = row[i], x1 = row[i + half];
         row[i] = x0 * c - x1 * s;

@@ -1315,10 +1315,12 @@ emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention
     a.keys = reinterpret_cast<float*>(p->keys);
     a.values = reinterpret_cast<float*>(p->values);
     a.position = reinterpret_cast<const int*>(p->position);
+    a.rope_position = reinterpret_cast<const int*>(p->rope_position);
     a.out = reinterpret_cast<float*>(out);
     a.partial = static_cast<float*>(partial);
     TRY(rope_table(h, p, &a.rope));
     if (h->recording) {
+        if (p->rope_position) return rec_unsupported(h, "a rotary position apart from the cache row");
         const int chunks = (p->context + kAttnChunk - 1) / kAttnChunk;
         if ((p->head_dim != 128 && p->head_dim != 256) || chunks > 1024)
             return rec_unsupported(h, "attention shape");

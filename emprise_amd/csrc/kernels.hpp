@@ -154,6 +154,7 @@ struct AttnArgs {
     float* keys;
     float* values;
     const int* position;
+    const int* rope_position;  // rotary position when it differs from *position, or null
     float* out;
     float* partial;  // scratch: [kv_heads][chunks][group][head_dim + 2]
     const float2* rope;  // [context][rotary / 2]: (cos, sin) of pos / base^(2i / rotary)

@@ -143,6 +143,71 @@ emprise_status emprise_model_last_hidden(emprise_model* m, float* hidden) {
     });
 }
 
+emprise_status emprise_model_last_hidden_normed(emprise_model* m, float* hidden) {
+    if (!m || !hidden) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] {
+        auto v = m->model->last_hidden_normed();
+        std::memcpy(hidden, v.data(), v.size() * sizeof(float));
+    });
+}
+
+emprise_status emprise_model_evaluate_block(emprise_model* m, const int* tokens, size_t n, float* logits) {
+    if (!m || !tokens || !logits) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] {
+        const auto rows = m->model->evaluate_block(std::vector<int>(tokens, tokens + n));
+        for (size_t i = 0; i < rows.size(); ++i)
+            std::memcpy(logits + i * rows[i].size(), rows[i].data(), rows[i].size() * sizeof(float));
+    });
+}
+
+int emprise_model_has_mtp(const emprise_model* m) { return m && m->model->has_mtp() ? 1 : 0; }
+
+emprise_status emprise_model_mtp_draft(emprise_model* m, const float* hidden, int token, size_t position,
+                                       float* logits) {
+    if (!m || !hidden || !logits) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    if (!m->model->has_mtp()) {
+        g_error = "The model has no MTP (nextn) block";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] {
+        const size_t H = static_cast<size_t>(m->model->info().hidden);
+        auto v = m->model->mtp_draft(std::vector<float>(hidden, hidden + H), token, position);
+        std::memcpy(logits, v.data(), v.size() * sizeof(float));
+    });
+}
+
+emprise_status emprise_model_mtp_hidden(emprise_model* m, float* hidden) {
+    if (!m || !hidden) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    if (!m->model->has_mtp()) {
+        g_error = "The model has no MTP (nextn) block";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] {
+        auto v = m->model->mtp_hidden();
+        std::memcpy(hidden, v.data(), v.size() * sizeof(float));
+    });
+}
+
+emprise_status emprise_model_reset_mtp(emprise_model* m) {
+    if (!m) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] { m->model->reset_mtp(); });
+}
+
 emprise_status emprise_model_generate(emprise_model* m, const int* prompt, size_t prompt_len, size_t count, int* tokens,
                                       size_t* emitted, double* arrivals) {
     if (!m || (!prompt && prompt_len) || (!tokens && count) || !emitted) {

@@ -143,6 +143,37 @@ Model::Model(const ModelOptions& options) : opt_(options) {
         for (const auto& n : names) per_token += g.tensor(p + n).bytes;
     }
     d.token_weight_bytes = per_token;
+    // the MTP block after the main layers, named blk.<layers> (blk.32 at the 9B shape,
+    // the name model.cpp:378-392 uses); not part of a decode step's weights
+    const std::string mp = "blk." + std::to_string(d.layers) + ".";
+    if (g.has(mp + "nextn.eh_proj.weight")) {
+        Mtp& M = mtp_;
+        Layer& L = M.layer;
+        M.eh = upload(mp + "nextn.eh_proj.weight", 2 * H, H);
+        M.enorm = upload_vector(mp + "nextn.enorm.weight", H);
+        M.hnorm = upload_vector(mp + "nextn.hnorm.weight", H);
+        M.head_norm = upload_vector(mp + "nextn.shared_head_norm.weight", H);
+        L.attn_norm = upload_vector(mp + "attn_norm.weight", H);
+        L.post_norm = upload_vector(mp + "post_attention_norm.weight", H);
+        L.q = upload(mp + "attn_q.weight", H, qd);
+        L.k = upload(mp + "attn_k.weight", H, kvd);
+        L.v = upload(mp + "attn_v.weight", H, kvd);
+        L.o = upload(mp + "attn_output.weight", uint64_t(d.heads) * d.head_dim, H);
+        L.q_norm = upload_vector(mp + "attn_q_norm.weight", d.head_dim);
+        L.k_norm = upload_vector(mp + "attn_k_norm.weight", d.head_dim);
+        L.gate = upload(mp + "ffn_gate.weight", H, d.ffn);
+        L.up = upload(mp + "ffn_up.weight", H, d.ffn);
+        L.down = upload(mp + "ffn_down.weight", d.ffn, H);
+        L.keys = backend_->dev_alloc(opt_.context * kvd * 4);
+        L.values = backend_->dev_alloc(opt_.context * kvd * 4);
+        M.cat = backend_->dev_alloc(2 * H * 4);
+        M.cur = backend_->dev_alloc(H * 4);
+        M.x = backend_->dev_alloc(H * 4);
+        M.in = backend_->dev_alloc(H * 4);
+        M.ctl = backend_->dev_alloc(4 * sizeof(int));
+        backend_->dev_fill(M.x, 0.f, H);
+        M.present = true;
+    }
     // activations
     const uint64_t wide = std::max<uint64_t>({H, qd + 2 * kvd, uint64_t(d.heads) * d.head_dim, vd});
     for (auto& x : x_) x = backend_->dev_alloc(H * 4);
@@ -388,6 +419,90 @@ std::vector<float> Model::last_hidden() {
     std::vector<float> h(static_cast<size_t>(info_.hidden));
     backend_->dev_download(h.data(), x_[last_x_], h.size() * 4);
     return h;
+}
+
+std::vector<float> Model::last_hidden_normed() {
+    const int H = info_.hidden;
+    backend_->dev_rmsnorm(x_[last_x_], output_norm_, tmp_, H, info_.eps);
+    std::vector<float> h(static_cast<size_t>(H));
+    backend_->dev_download(h.data(), tmp_, h.size() * 4);
+    return h;
+}
+
+// Model::Impl::mtp_step (model.cpp:376-397): cur = eh_proj [enorm(embed(token)) |
+// hnorm(hidden)]; the block's attention (its own cache, one more row per call, rotary
+// position `position`) and FFN add to cur, which is kept as mtp_hidden; logits = output
+// head of the shared head norm of cur. The reference's unfused FFN (mm, silu * up, mm)
+// runs here as the fused feed-forward op, the same arithmetic per element.
+std::vector<float> Model::mtp_draft(const std::vector<float>& hidden, int token, size_t position) {
+    const emprise_model_info& d = info_;
+    if (!mtp_.present) throw std::runtime_error("The model has no MTP (nextn) block");
+    if (hidden.size() != static_cast<size_t>(d.hidden)) throw std::invalid_argument("MTP hidden size");
+    if (token < 0 || token >= d.vocab) throw std::out_of_range("Token ID");
+    if (position >= opt_.context) throw std::invalid_argument("MTP position outside the context");
+    if (mtp_.length >= opt_.context) throw std::runtime_error("MTP context budget exhausted");
+    HipBackend& b = *backend_;
+    Mtp& M = mtp_;
+    const Layer& L = M.layer;
+    const uint64_t H = d.hidden, qd = uint64_t(d.heads) * d.head_dim * 2, kvd = uint64_t(d.kv_heads) * d.head_dim;
+    const int ctl[4] = {static_cast<int>(M.length), static_cast<int>(position), token, 0};
+    b.dev_upload(M.ctl, ctl, sizeof ctl);
+    b.dev_upload(M.in, hidden.data(), H * 4);
+    b.dev_embed(embd_, M.ctl + 2 * sizeof(int), tmp_);
+    b.dev_rmsnorm(tmp_, M.enorm, M.cat, static_cast<int>(H), d.eps);
+    b.dev_rmsnorm(M.in, M.hnorm, M.cat + H * 4, static_cast<int>(H), d.eps);
+    b.dev_linear(M.eh, M.cat, M.cur);
+    const emprise_hip_input in{M.cur, 0, 0, L.attn_norm, d.eps};
+    const emprise_weight w[3] = {L.q, L.k, L.v};
+    const emprise_dev parts[3] = {qkv_, qkv_ + qd * 4, qkv_ + (qd + kvd) * 4};
+    b.dev_linear_norm(in, 3, w, parts);
+    emprise_hip_attention_params p{};
+    p.heads = d.heads;
+    p.kv_heads = d.kv_heads;
+    p.head_dim = d.head_dim;
+    p.rotary = d.rotary;
+    p.context = static_cast<int>(opt_.context);
+    p.eps = d.eps;
+    p.rope_base = d.rope_base;
+    p.q_norm = L.q_norm;
+    p.k_norm = L.k_norm;
+    p.keys = L.keys;
+    p.values = L.values;
+    p.position = M.ctl;
+    p.rope_position = M.ctl + sizeof(int);
+    b.dev_attention(p, qkv_, attn_out_);
+    b.dev_linear(L.o, attn_out_, delta_attn_);
+    const emprise_hip_input fin{M.cur, delta_attn_, M.x, L.post_norm, d.eps};
+    b.dev_ffn(&fin, 0, L.gate, L.up, L.down, delta_ffn_);
+    b.dev_add(M.x, delta_ffn_, static_cast<int>(H));
+    const emprise_hip_input hin{M.x, 0, 0, M.head_norm, d.eps};
+    b.dev_linear_norm(hin, 1, &output_, &logits_);
+    ++M.length;
+    std::vector<float> out(static_cast<size_t>(d.vocab));
+    b.dev_download(out.data(), logits_, out.size() * 4);
+    return out;
+}
+
+std::vector<float> Model::mtp_hidden() {
+    if (!mtp_.present) throw std::runtime_error("The model has no MTP (nextn) block");
+    std::vector<float> h(static_cast<size_t>(info_.hidden));
+    backend_->dev_download(h.data(), mtp_.x, h.size() * 4);
+    return h;
+}
+
+// Every position's logits, positions evaluated in order as decode steps (the reference
+// batches the projections of the block, model.cpp:274-354; per position the arithmetic is
+// the same, so the logits agree up to summation order).
+std::vector<std::vector<float>> Model::evaluate_block(const std::vector<int>& tokens) {
+    if (tokens.empty()) throw std::invalid_argument("Empty block");
+    if (tokens.size() > opt_.context - std::min(position_, opt_.context))
+        throw std::runtime_error("Context budget exhausted");
+    for (int t : tokens)
+        if (t < 0 || t >= info_.vocab) throw std::out_of_range("Token ID");
+    std::vector<std::vector<float>> out;
+    out.reserve(tokens.size());
+    for (int t : tokens) out.push_back(evaluate(t, true));
+    return out;
 }
 
 // Positions [start, start + count) of the tokens at dev_prompt_ (token of position p at

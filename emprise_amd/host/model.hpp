@@ -45,6 +45,18 @@ public:
     std::vector<int> generate(const std::vector<int>& prompt, size_t count, std::vector<double>* arrivals);
     // Model::prefill: tokens from the current position on; the last one's logits
     std::vector<float> prefill(const std::vector<int>& tokens, bool want_logits = true);
+    // Model::evaluate_block (model.cpp:274-354, every position's logits): the tokens from
+    // the current position on, in order; one row of logits per token
+    std::vector<std::vector<float>> evaluate_block(const std::vector<int>& tokens);
+    // Model::last_hidden (model.cpp:483): the last residual through the output norm
+    // (last_hidden() above is last_hidden_raw)
+    std::vector<float> last_hidden_normed();
+    // The MTP (next-n) draft head, Model::mtp_draft / mtp_hidden / reset_mtp
+    // (model.cpp:376-397, :485-487), when the file has the block
+    bool has_mtp() const { return mtp_.present; }
+    std::vector<float> mtp_draft(const std::vector<float>& hidden, int token, size_t position);
+    std::vector<float> mtp_hidden();
+    void reset_mtp() { mtp_.length = 0; }
 
 private:
     struct Layer {
@@ -79,6 +91,17 @@ private:
     size_t pf_rows_ = 0;
     emprise_dev pf_x_ = 0, pf_xn_ = 0, pf_a_ = 0, pf_b_ = 0, pf_c_ = 0;
     bool have_graph_full_ = false, have_graph_prefill_ = false;
+    // the MTP block: its weights (an attention layer + FFN in `layer`), its own K/V cache
+    // of `length` rows, and buffers: cat = [enorm(e) | hnorm(h)], cur = eh_proj(cat), x =
+    // the block's output (Model::mtp_hidden), in = the caller's hidden, ctl = {cache row,
+    // rotary position, token}
+    struct Mtp {
+        bool present = false;
+        emprise_weight enorm = 0, hnorm = 0, eh = 0, head_norm = 0;
+        Layer layer;
+        size_t length = 0;
+        emprise_dev cat = 0, cur = 0, x = 0, in = 0, ctl = 0;
+    } mtp_;
     int step_program_ = -1;  // 1: step graphs are persistent programs, 0: per-op graphs, -1: none yet
 
 public:

@@ -219,6 +219,26 @@ void synth_write(const emprise_synth_config& c, const std::string& path) {
         mat(p + "ffn_up.weight", H, c.ffn);
         mat(p + "ffn_down.weight", c.ffn, H);
     }
+    if (c.mtp) {
+        // the next-n block after the main layers: an attention layer + FFN, fed by
+        // eh_proj over [enorm(embedding) | hnorm(hidden)]
+        const std::string p = "blk." + std::to_string(c.layers) + ".";
+        vec(p + "nextn.enorm.weight", {H}, 1);
+        vec(p + "nextn.hnorm.weight", {H}, 1);
+        mat(p + "nextn.eh_proj.weight", 2 * H, H);
+        vec(p + "nextn.shared_head_norm.weight", {H}, 1);
+        vec(p + "attn_norm.weight", {H}, 1);
+        mat(p + "attn_q.weight", H, qd);
+        mat(p + "attn_k.weight", H, kvd);
+        mat(p + "attn_v.weight", H, kvd);
+        mat(p + "attn_output.weight", uint64_t(c.heads) * c.head_dim, H);
+        vec(p + "attn_q_norm.weight", {uint64_t(c.head_dim)}, 1);
+        vec(p + "attn_k_norm.weight", {uint64_t(c.head_dim)}, 1);
+        vec(p + "post_attention_norm.weight", {H}, 1);
+        mat(p + "ffn_gate.weight", H, c.ffn);
+        mat(p + "ffn_up.weight", H, c.ffn);
+        mat(p + "ffn_down.weight", c.ffn, H);
+    }
     vec("output_norm.weight", {H}, 1);
     mat("output.weight", H, c.vocab);
     const uint64_t align = 32;
@@ -233,7 +253,7 @@ void synth_write(const emprise_synth_config& c, const std::string& path) {
     if (!f) throw std::runtime_error("Cannot write " + path);
     Writer w{f};
     try {
-        const int kv_count = 22;
+        const int kv_count = 22 + (c.mtp ? 1 : 0);
         w.put<uint32_t>(0x46554747u);
         w.put<uint32_t>(3);
         w.put<uint64_t>(ts.size());
@@ -242,7 +262,8 @@ void synth_write(const emprise_synth_config& c, const std::string& path) {
         w.kv_u32("general.alignment", static_cast<uint32_t>(align));
         w.kv_u64("emprise.synthetic.seed", c.seed);
         w.kv_u32("qwen35.embedding_length", static_cast<uint32_t>(c.hidden));
-        w.kv_u32("qwen35.block_count", static_cast<uint32_t>(c.layers));
+        w.kv_u32("qwen35.block_count", static_cast<uint32_t>(c.layers + (c.mtp ? 1 : 0)));
+        if (c.mtp) w.kv_u32("qwen35.nextn_predict_layers", 1);
         w.kv_u32("qwen35.feed_forward_length", static_cast<uint32_t>(c.ffn));
         w.kv_u32("qwen35.context_length", static_cast<uint32_t>(c.context_length));
         w.kv_u32("qwen35.attention.head_count", static_cast<uint32_t>(c.heads));

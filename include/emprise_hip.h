@@ -229,13 +229,17 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
  * back to back: q|gate interleaved per head (heads*head_dim*2), then k and v
  * (kv_heads*head_dim each). The new k (after RMSNorm + RoPE) and v are stored at
  * *position (device int32) of the caches keys/values (context*kv_heads*head_dim floats
- * each), then every head attends over positions 0..*position. out = heads*head_dim. */
+ * each), then every head attends over positions 0..*position. out = heads*head_dim.
+ * rope_position (device int32, or 0 for *position) is the rotary position when it differs
+ * from the cache row: the MTP block's own cache grows by one row per draft while it
+ * rotates at the caller's position (model.cpp:383-385, attention_preout's pos). */
 typedef struct {
     int heads, kv_heads, head_dim, rotary, context;
     float eps, rope_base;
     emprise_weight q_norm, k_norm;
     emprise_dev keys, values;
     emprise_dev position;
+    emprise_dev rope_position;
 } emprise_hip_attention_params;
 emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention_params* p, emprise_dev qkv,
                                      emprise_dev out);

@@ -77,6 +77,25 @@ emprise_status emprise_model_evaluate(emprise_model* m, int token, float* logits
 emprise_status emprise_model_prefill(emprise_model* m, const int* tokens, size_t n, float* logits);
 /* The residual stream after the last evaluated position (Model::last_hidden_raw). */
 emprise_status emprise_model_last_hidden(emprise_model* m, float* hidden);
+/* Model::last_hidden (model.cpp:483): that residual through the output norm. */
+emprise_status emprise_model_last_hidden_normed(emprise_model* m, float* hidden);
+/* Model::evaluate_block (model.hpp:37-39, model.cpp:274-354): the n tokens from the
+ * current position on, in order, with every position's logits (n rows of vocab floats;
+ * the reference's draft-verification call). */
+emprise_status emprise_model_evaluate_block(emprise_model* m, const int* tokens, size_t n, float* logits);
+
+/* The MTP (next-n) draft head (model.hpp:42-48; model.cpp:376-397, :485-487), present
+ * when the file has blk.<layers>.nextn.* (blk.32 at the 9B shape). */
+int emprise_model_has_mtp(const emprise_model* m);
+/* Model::mtp_draft: from a hidden vector (hidden floats) and the token that followed it,
+ * the logits (vocab floats) of the token after; the block's attention appends one row to
+ * its own cache and rotates at `position`. EINVAL without the block. */
+emprise_status emprise_model_mtp_draft(emprise_model* m, const float* hidden, int token, size_t position,
+                                       float* logits);
+/* Model::mtp_hidden: the block's output of the last draft (before the shared head norm). */
+emprise_status emprise_model_mtp_hidden(emprise_model* m, float* hidden);
+/* Model::reset_mtp: the block's cache emptied. */
+emprise_status emprise_model_reset_mtp(emprise_model* m);
 
 /* Model::generate (model.cpp:488-503): prefill, then greedy tokens until count or EOS.
  * tokens receives up to count ids, *emitted the number written, arrivals (optional,
@@ -104,6 +123,7 @@ typedef struct {
     int eos;
     uint32_t matrix_type; /* EMPRISE_Q6_K or EMPRISE_Q4_K for every matrix */
     int q4_k_m_mix;       /* 1: attn_v and ffn_down Q6_K, every other matrix Q4_K */
+    int mtp;              /* 1: add the MTP (next-n) block blk.<layers> (qwen35.nextn_predict_layers = 1) */
 } emprise_synth_config;
 
 /* Writes a GGUF v3 file with deterministic weights: counter-based SplitMix64 streams per

@@ -68,6 +68,15 @@ def lib() -> ctypes.CDLL:
         L.eo_model_generate.argtypes = [vp, ctypes.POINTER(ctypes.c_int), sz, sz, ctypes.POINTER(ctypes.c_int), _fp]
         L.eo_model_last_hidden.restype = i32
         L.eo_model_last_hidden.argtypes = [vp, _fp]
+        L.eo_model_last_hidden_normed.restype = i32
+        L.eo_model_last_hidden_normed.argtypes = [vp, _fp]
+        L.eo_model_has_mtp.restype = i32
+        L.eo_model_has_mtp.argtypes = [vp]
+        L.eo_model_reset_mtp.argtypes = [vp]
+        L.eo_model_mtp_draft.restype = i32
+        L.eo_model_mtp_draft.argtypes = [vp, _fp, i32, sz, _fp]
+        L.eo_model_mtp_hidden.restype = i32
+        L.eo_model_mtp_hidden.argtypes = [vp, _fp]
         L.eo_quantize_q8.argtypes = [_fp, sz, _fp]
         L.eo_model_seek.restype = i32
         L.eo_model_seek.argtypes = [vp, sz]
@@ -233,10 +242,31 @@ class Model:
         if lib().eo_model_seek(self.m, position):
             raise RuntimeError(lib().eo_last_error().decode())
 
-    def last_hidden(self) -> np.ndarray:
+    def last_hidden(self, normed: bool = False) -> np.ndarray:
         out = np.empty(self.hidden, dtype=np.float32)
-        lib().eo_model_last_hidden(self.m, _f(out))
+        (lib().eo_model_last_hidden_normed if normed else lib().eo_model_last_hidden)(self.m, _f(out))
         return out
+
+    @property
+    def has_mtp(self) -> bool:
+        return bool(lib().eo_model_has_mtp(self.m))
+
+    def mtp_draft(self, hidden, token: int, position: int) -> np.ndarray:
+        """Model::mtp_draft (model.cpp:376-397)."""
+        h = np.ascontiguousarray(hidden, dtype=np.float32)
+        out = np.empty(self.vocab, dtype=np.float32)
+        if lib().eo_model_mtp_draft(self.m, _f(h), token, position, _f(out)):
+            raise RuntimeError(lib().eo_last_error().decode())
+        return out
+
+    def mtp_hidden(self) -> np.ndarray:
+        out = np.empty(self.hidden, dtype=np.float32)
+        if lib().eo_model_mtp_hidden(self.m, _f(out)):
+            raise RuntimeError(lib().eo_last_error().decode())
+        return out
+
+    def reset_mtp(self):
+        lib().eo_model_reset_mtp(self.m)
 
     def generate(self, prompt, count: int):
         p = (ctypes.c_int * len(prompt))(*prompt)

@@ -430,6 +430,16 @@ struct eo_model {
     float* output_norm;
     float* last_hidden;
     int q8; /* --fast-q8: Q6_K projections see quantised inputs */
+    /* the MTP (next-n) block, blk.<layers> (model.cpp:376-397), when the file has one:
+     * an attention layer plus the nextn embedding/hidden norms, eh_proj [2H -> H] and the
+     * shared head norm; its own K/V cache (mtp_state) and last output (mtp_hidden) */
+    int has_mtp;
+    eo_layer mtp;
+    const uint8_t* eh;
+    uint32_t teh;
+    float *enorm, *hnorm, *head_norm;
+    eo_layer_state mtp_state;
+    float* mtp_hidden;
 };
 
 static const eo_kv* find_kv(const eo_model* m, const char* key) {
@@ -464,6 +474,10 @@ void eo_model_free(eo_model* m) {
     free(m->state);
     free(m->output_norm);
     free(m->last_hidden);
+    free(m->mtp.attn_norm); free(m->mtp.post_norm); free(m->mtp.q_norm); free(m->mtp.k_norm);
+    free(m->enorm); free(m->hnorm); free(m->head_norm);
+    free(m->mtp_state.keys); free(m->mtp_state.values);
+    free(m->mtp_hidden);
     free(m);
 }
 
@@ -672,6 +686,35 @@ eo_model* eo_model_load(const char* path, size_t context, int threads, char* err
             m->state[l].keys = (float*)malloc(context * (size_t)kvd * sizeof(float));
             m->state[l].values = (float*)malloc(context * (size_t)kvd * sizeof(float));
             if (!m->state[l].keys || !m->state[l].values) { set_err("Out of memory for KV cache"); goto fail; }
+        }
+    }
+    {
+        /* the MTP block, named after the last main layer index + 1 (blk.32 at the 9B
+         * shape, the name model.cpp:378-392 uses) */
+        const int l = m->layers;
+        if (find_tensor(m, NAME("nextn.eh_proj.weight"))) {
+            eo_layer* L = &m->mtp;
+            if (matrix(m, NAME("nextn.eh_proj.weight"), 2 * (uint64_t)H, (uint64_t)H, &m->eh, &m->teh) ||
+                !(m->enorm = param(m, NAME("nextn.enorm.weight"), (uint64_t)H)) ||
+                !(m->hnorm = param(m, NAME("nextn.hnorm.weight"), (uint64_t)H)) ||
+                !(m->head_norm = param(m, NAME("nextn.shared_head_norm.weight"), (uint64_t)H)) ||
+                !(L->attn_norm = param(m, NAME("attn_norm.weight"), (uint64_t)H)) ||
+                !(L->post_norm = param(m, NAME("post_attention_norm.weight"), (uint64_t)H)) ||
+                !(L->q_norm = param(m, NAME("attn_q_norm.weight"), (uint64_t)m->head_dim)) ||
+                !(L->k_norm = param(m, NAME("attn_k_norm.weight"), (uint64_t)m->head_dim)) ||
+                matrix(m, NAME("attn_q.weight"), (uint64_t)H, (uint64_t)qd, &L->q, &L->tq) ||
+                matrix(m, NAME("attn_k.weight"), (uint64_t)H, (uint64_t)kvd, &L->k, &L->tk) ||
+                matrix(m, NAME("attn_v.weight"), (uint64_t)H, (uint64_t)kvd, &L->v, &L->tv) ||
+                matrix(m, NAME("attn_output.weight"), (uint64_t)m->heads * m->head_dim, (uint64_t)H, &L->o, &L->to) ||
+                matrix(m, NAME("ffn_gate.weight"), (uint64_t)H, (uint64_t)m->ffn, &L->fg, &L->tfg) ||
+                matrix(m, NAME("ffn_up.weight"), (uint64_t)H, (uint64_t)m->ffn, &L->fu, &L->tfu) ||
+                matrix(m, NAME("ffn_down.weight"), (uint64_t)m->ffn, (uint64_t)H, &L->fd, &L->tfd))
+                goto fail;
+            m->mtp_state.keys = (float*)malloc(context * (size_t)kvd * sizeof(float));
+            m->mtp_state.values = (float*)malloc(context * (size_t)kvd * sizeof(float));
+            m->mtp_hidden = (float*)calloc((size_t)H, sizeof(float));
+            if (!m->mtp_state.keys || !m->mtp_state.values || !m->mtp_hidden) { set_err("Out of memory for MTP"); goto fail; }
+            m->has_mtp = 1;
         }
     }
 #undef NAME
@@ -950,6 +993,90 @@ int eo_model_evaluate_many(eo_model* m, const int* tokens, size_t n, float* logi
     }
     free(x); free(nrm); free(attn); free(b0); free(b1); free(b2); free(b3); free(b4); free(g); free(u);
     return rc;
+}
+
+int eo_model_has_mtp(const eo_model* m) { return m->has_mtp; }
+
+/* Model::reset_mtp (model.cpp:487): the MTP block's attention cache emptied */
+void eo_model_reset_mtp(eo_model* m) { m->mtp_state.length = 0; }
+
+/* Model::Impl::mtp_step (model.cpp:376-397): the next-n draft head. From the caller's
+ * hidden vector and token: [enorm(embed(token)) | hnorm(hidden)] through eh_proj, one
+ * attention block (the main attention's arithmetic at rotary position `pos`, over the
+ * block's own cache, which grows by one row per call), the unfused SwiGLU FFN, then the
+ * shared head norm and the output head. The block's output before the head norm is kept
+ * (Model::mtp_hidden). Projections follow mlinear (--fast-q8 as the main path). */
+int eo_model_mtp_draft(eo_model* m, const float* hidden, int token, size_t pos, float* logits) {
+    if (!m->has_mtp) { set_err("The model has no MTP (nextn) block"); return -1; }
+    if (token < 0 || token >= m->vocab) { set_err("Token ID"); return -1; }
+    if (m->mtp_state.length >= m->context) { set_err("MTP context budget exhausted"); return -1; }
+    const size_t H = (size_t)m->hidden, F = (size_t)m->ffn, kvd = (size_t)m->kv_heads * m->head_dim;
+    const size_t qd = (size_t)m->heads * m->head_dim * 2, ad = (size_t)m->heads * m->head_dim;
+    const eo_layer* L = &m->mtp;
+    const size_t row_bytes = eo_encoded_bytes(m->tembd, H);
+    float* cat = (float*)malloc(2 * H * sizeof(float));
+    float* cur = (float*)malloc(H * sizeof(float));
+    float* nrm = (float*)malloc(H * sizeof(float));
+    float* t = (float*)malloc(H * sizeof(float));
+    float* q = (float*)malloc(qd * sizeof(float));
+    float* k = (float*)malloc(kvd * sizeof(float));
+    float* v = (float*)malloc(kvd * sizeof(float));
+    float* ao = (float*)malloc(ad * sizeof(float));
+    float* g = (float*)malloc(F * sizeof(float));
+    float* u = (float*)malloc(F * sizeof(float));
+    int rc = eo_dequantize(m->tembd, m->embd + (size_t)token * row_bytes, row_bytes, cat, H);
+    if (!rc) {
+        eo_rms(cat, H, m->enorm, m->eps);
+        memcpy(cat + H, hidden, H * sizeof(float));
+        eo_rms(cat + H, H, m->hnorm, m->eps);
+        rc = mlinear(m, m->teh, m->eh, cat, 2 * H, cur, H);
+    }
+    if (!rc) {
+        memcpy(nrm, cur, H * sizeof(float));
+        eo_rms(nrm, H, L->attn_norm, m->eps);
+        rc = mlinear(m, L->tq, L->q, nrm, H, q, qd);
+        if (!rc) rc = mlinear(m, L->tk, L->k, nrm, H, k, kvd);
+        if (!rc) rc = mlinear(m, L->tv, L->v, nrm, H, v, kvd);
+    }
+    if (!rc) {
+        m->mtp_state.length += 1;
+        eo_attention(m->heads, m->kv_heads, m->head_dim, m->rotary, m->rope_base, m->eps, L->q_norm, L->k_norm, q, k,
+                     v, m->mtp_state.keys, m->mtp_state.values, m->mtp_state.length, (int)pos, ao);
+        rc = mlinear(m, L->to, L->o, ao, ad, t, H);
+    }
+    if (!rc) {
+        for (size_t i = 0; i < H; ++i) cur[i] += t[i];
+        memcpy(nrm, cur, H * sizeof(float));
+        eo_rms(nrm, H, L->post_norm, m->eps);
+        rc = mlinear(m, L->tfg, L->fg, nrm, H, g, F);
+        if (!rc) rc = mlinear(m, L->tfu, L->fu, nrm, H, u, F);
+    }
+    if (!rc) {
+        for (size_t i = 0; i < F; ++i) g[i] = eo_silu(g[i]) * u[i];
+        rc = mlinear(m, L->tfd, L->fd, g, F, t, H);
+    }
+    if (!rc) {
+        for (size_t i = 0; i < H; ++i) cur[i] += t[i];
+        memcpy(m->mtp_hidden, cur, H * sizeof(float));
+        eo_rms(cur, H, m->head_norm, m->eps);
+        if (logits) rc = mlinear(m, m->toutput, m->output, cur, H, logits, (size_t)m->vocab);
+    }
+    free(cat); free(cur); free(nrm); free(t); free(q); free(k); free(v); free(ao); free(g); free(u);
+    return rc;
+}
+
+int eo_model_mtp_hidden(const eo_model* m, float* out) {
+    if (!m->has_mtp) { set_err("The model has no MTP (nextn) block"); return -1; }
+    memcpy(out, m->mtp_hidden, (size_t)m->hidden * sizeof(float));
+    return 0;
+}
+
+/* Model::last_hidden (model.cpp:483): the last residual through the output norm, the
+ * vector the output head multiplies (evaluate's hidden_out, model.cpp:248-251). */
+int eo_model_last_hidden_normed(const eo_model* m, float* out) {
+    memcpy(out, m->last_hidden, (size_t)m->hidden * sizeof(float));
+    eo_rms(out, (size_t)m->hidden, m->output_norm, m->eps);
+    return 0;
 }
 
 int eo_model_last_hidden(const eo_model* m, float* out) {

@@ -107,6 +107,14 @@ int eo_model_generate(eo_model* m, const int* prompt, size_t prompt_len, size_t 
                       int* tokens, float* margins);
 /* Layer trace of the last evaluate: the residual after layer `layer` (l_out). */
 int eo_model_last_hidden(const eo_model* m, float* out);
+/* Model::last_hidden (model.cpp:483): that residual through the output norm. */
+int eo_model_last_hidden_normed(const eo_model* m, float* out);
+/* The MTP (next-n) draft head, Model::mtp_draft / mtp_hidden / reset_mtp
+ * (model.cpp:376-397, :485-487): blk.<layers>.nextn.* + that block's attention and FFN. */
+int eo_model_has_mtp(const eo_model* m);
+void eo_model_reset_mtp(eo_model* m);
+int eo_model_mtp_draft(eo_model* m, const float* hidden, int token, size_t pos, float* logits);
+int eo_model_mtp_hidden(const eo_model* m, float* out);
 const char* eo_last_error(void);
 
 #ifdef __cplusplus

@@ -221,3 +221,131 @@ def test_quantize_q8_matches_core_rule():
     t = got[201 * 32:202 * 32]
     assert t[1] == -15.0 and t[16] == 1.0 and t[15] == -1.0 and t[31] == 16.0
     assert not got[200 * 32:201 * 32].any()
+
+
+# ---- the MTP draft head (model.cpp:376-397) on F32 models built to reduce it to closed forms
+
+def _mtp_model(tmp_path, rng, eh="hidden", attn_out=False, ffn=False, name="mtp.gguf"):
+    """One attention layer (unused by the draft) + the MTP block blk.1, H = 8 = 2 heads x 4,
+    1 kv head, ffn 8, vocab 16. eh_proj selects one half of [enorm(e) | hnorm(h)]; the
+    block's attention output and FFN down projections are zero unless asked for."""
+    from gguf_f32 import write
+    H, V, F, hd = 8, 16, 8, 4
+    meta = {"embedding_length": H, "block_count": 2, "nextn_predict_layers": 1, "feed_forward_length": F,
+            "context_length": 64, "attention.head_count": 2, "attention.head_count_kv": 1,
+            "attention.key_length": hd, "attention.value_length": hd, "rope.dimension_count": 2,
+            "rope.freq_base": 10000.0, "attention.layer_norm_rms_epsilon": 1e-6, "ssm.group_count": 1,
+            "ssm.time_step_rank": 1, "ssm.state_size": 4, "ssm.conv_kernel": 4, "eos": V}
+    n = lambda *s: rng.standard_normal(s).astype(np.float32)
+    w = lambda: (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    t = {"token_embd.weight": n(V, H), "output_norm.weight": w(), "output.weight": n(V, H)}
+    for p in ("blk.0.", "blk.1."):
+        t.update({p + "attn_norm.weight": w(), p + "post_attention_norm.weight": w(),
+                  p + "attn_q.weight": n(2 * 2 * hd, H), p + "attn_k.weight": n(hd, H), p + "attn_v.weight": n(hd, H),
+                  p + "attn_q_norm.weight": w()[:hd].copy(), p + "attn_k_norm.weight": w()[:hd].copy(),
+                  p + "ffn_gate.weight": n(F, H), p + "ffn_up.weight": n(F, H)})
+    t["blk.0.attn_output.weight"], t["blk.0.ffn_down.weight"] = n(H, H), n(H, F)
+    t["blk.1.attn_output.weight"] = np.eye(H, dtype=np.float32) if attn_out else np.zeros((H, H), np.float32)
+    t["blk.1.ffn_down.weight"] = n(H, F) if ffn else np.zeros((H, F), np.float32)
+    sel = np.zeros((H, 2 * H), np.float32)
+    sel[:, H:] = np.eye(H) if eh == "hidden" else 0
+    sel[:, :H] = np.eye(H) if eh == "embedding" else 0
+    t["blk.1.nextn.eh_proj.weight"] = sel
+    t.update({"blk.1.nextn.enorm.weight": w(), "blk.1.nextn.hnorm.weight": w(),
+              "blk.1.nextn.shared_head_norm.weight": w()})
+    p = tmp_path / name
+    write(p, meta, t)
+    return p, t
+
+
+def _rms64(x, w, eps=1e-6):
+    x = x.astype(np.float64)
+    return x / np.sqrt(np.mean(x * x) + eps) * w
+
+
+def _close64(got, want, rel=1e-5):
+    assert np.max(np.abs(got - want)) <= rel * np.max(np.abs(want)), (got, want)
+
+
+def test_mtp_hidden_half_and_head(tmp_path):
+    """eh_proj = [0 | I], attention output and FFN down zero: the block's output is
+    hnorm(hidden) and the logits are output . head_norm(hnorm(hidden)). The embedding half
+    and the block's residual branches contribute nothing."""
+    rng = np.random.default_rng(7)
+    path, t = _mtp_model(tmp_path, rng, eh="hidden")
+    m = oracle.Model(str(path), context=64)
+    assert m.has_mtp
+    h = rng.standard_normal(8).astype(np.float32)
+    logits = m.mtp_draft(h, 3, 5)
+    cur = _rms64(h, t["blk.1.nextn.hnorm.weight"])
+    _close64(m.mtp_hidden(), cur)
+    _close64(logits, t["output.weight"] @ _rms64(cur, t["blk.1.nextn.shared_head_norm.weight"]))
+
+
+def test_mtp_embedding_half(tmp_path):
+    """eh_proj = [I | 0]: the block's output is enorm(embedding row of the token),
+    whatever the hidden vector."""
+    rng = np.random.default_rng(8)
+    path, t = _mtp_model(tmp_path, rng, eh="embedding")
+    m = oracle.Model(str(path), context=64)
+    for token in (0, 11):
+        m.reset_mtp()
+        m.mtp_draft(rng.standard_normal(8).astype(np.float32), token, 9)
+        _close64(m.mtp_hidden(), _rms64(t["token_embd.weight"][token], t["blk.1.nextn.enorm.weight"]))
+
+
+def test_mtp_attention_first_row(tmp_path):
+    """The first draft after reset_mtp attends over one row, so each head's output is
+    v of its kv head times sigmoid of its gate (the second half of the head's q
+    projection); with attn_output = I it is added to the block's input."""
+    rng = np.random.default_rng(9)
+    path, t = _mtp_model(tmp_path, rng, eh="embedding", attn_out=True)
+    m = oracle.Model(str(path), context=64)
+    token = 5
+    m.mtp_draft(rng.standard_normal(8).astype(np.float32), token, 17)
+    cur = _rms64(t["token_embd.weight"][token], t["blk.1.nextn.enorm.weight"])
+    a = _rms64(cur, t["blk.1.attn_norm.weight"])
+    qg = t["blk.1.attn_q.weight"].astype(np.float64) @ a
+    v = t["blk.1.attn_v.weight"].astype(np.float64) @ a
+    o = np.concatenate([v / (1 + np.exp(-qg[h * 8 + 4:h * 8 + 8])) for h in range(2)])
+    _close64(m.mtp_hidden(), cur + o)
+
+
+def test_mtp_feed_forward(tmp_path):
+    """With the attention output zero, the block adds down(silu(gate p) * up p) with p =
+    post_norm(rms(block input))."""
+    rng = np.random.default_rng(10)
+    path, t = _mtp_model(tmp_path, rng, eh="hidden", ffn=True)
+    m = oracle.Model(str(path), context=64)
+    h = rng.standard_normal(8).astype(np.float32)
+    m.mtp_draft(h, 2, 3)
+    cur = _rms64(h, t["blk.1.nextn.hnorm.weight"])
+    p = _rms64(cur, t["blk.1.post_attention_norm.weight"])
+    g, u = t["blk.1.ffn_gate.weight"] @ p, t["blk.1.ffn_up.weight"] @ p
+    _close64(m.mtp_hidden(), cur + t["blk.1.ffn_down.weight"].astype(np.float64) @ (g / (1 + np.exp(-g)) * u))
+
+
+def test_mtp_cache_grows_until_reset(tmp_path):
+    """Without reset_mtp the block's cache keeps every draft's row: a draft of token 9
+    after one of token 4 attends over both rows and differs from the same draft on an
+    empty cache; after reset_mtp a repeated draft gives the first one's bits."""
+    rng = np.random.default_rng(11)
+    path, _ = _mtp_model(tmp_path, rng, eh="embedding", attn_out=True)
+    m = oracle.Model(str(path), context=64)
+    h = rng.standard_normal(8).astype(np.float32)
+    first = m.mtp_draft(h, 4, 6)
+    chained = m.mtp_draft(h, 9, 7)
+    m.reset_mtp()
+    alone = m.mtp_draft(h, 9, 7)
+    assert not np.allclose(chained, alone)
+    m.reset_mtp()
+    assert np.array_equal(m.mtp_draft(h, 4, 6).view(np.uint32), first.view(np.uint32))
+
+
+def test_last_hidden_normed_is_output_norm_of_raw(tmp_path):
+    """Model::last_hidden is the last residual through the output norm."""
+    rng = np.random.default_rng(12)
+    path, t = _mtp_model(tmp_path, rng)
+    m = oracle.Model(str(path), context=64)
+    m.evaluate(1)
+    _close64(m.last_hidden(normed=True), _rms64(m.last_hidden(), t["output_norm.weight"]))
