@@ -29,6 +29,12 @@
  *   eo_quantize_q8     core.cpp:119-125's construction of the checked input; fp16(s) by
  *                      the test's monotone search (core.cpp:14-21), tested against numpy's
  *                      float16 rounding and the GPU's standalone quantiser bit for bit
+ *   eo_model_evaluate_many  bit-equal to eo_model_evaluate position by position (logits,
+ *                      last residual, the state left behind), plain and Q8
+ *   eo_model_mtp_*     closed forms on F32 models built for them: each half of the
+ *                      [enorm(e) | hnorm(h)] input, the one-row attention (v times the
+ *                      sigmoid gate), the FFN, the head; cache growth and reset
+ *   eo_model_last_hidden_normed  the output norm of eo_model_last_hidden
  */
 #ifndef EMPRISE_ORACLE_H
 #define EMPRISE_ORACLE_H
