@@ -405,7 +405,8 @@ class SynthConfig(ctypes.Structure):
                 ("value_heads", ctypes.c_int), ("state_dim", ctypes.c_int), ("conv_width", ctypes.c_int),
                 ("full_attention_interval", ctypes.c_int), ("context_length", ctypes.c_int),
                 ("rope_base", ctypes.c_float), ("eps", ctypes.c_float), ("eos", ctypes.c_int),
-                ("matrix_type", ctypes.c_uint32), ("q4_k_m_mix", ctypes.c_int), ("mtp", ctypes.c_int)]
+                ("matrix_type", ctypes.c_uint32), ("q4_k_m_mix", ctypes.c_int), ("mtp", ctypes.c_int),
+                ("tokenizer", ctypes.c_int)]
 
 
 # The benchmark's model shapes. TINY is config 0 (hidden 512, 4 layers GDN,GDN,GDN,attention,
@@ -449,6 +450,19 @@ def host_lib() -> ctypes.CDLL:
     lib.emprise_model_evaluate.argtypes = [vp, ctypes.c_int, P(ctypes.c_float)]
     lib.emprise_model_last_hidden.restype = ctypes.c_int
     lib.emprise_model_last_hidden.argtypes = [vp, P(ctypes.c_float)]
+    lib.emprise_tokenizer_open.restype = ctypes.c_int
+    lib.emprise_tokenizer_open.argtypes = [ctypes.c_char_p, P(vp)]
+    lib.emprise_tokenizer_close.argtypes = [vp]
+    lib.emprise_model_tokenizer.restype = vp
+    lib.emprise_model_tokenizer.argtypes = [vp]
+    lib.emprise_tokenizer_encode.restype = ctypes.c_int
+    lib.emprise_tokenizer_encode.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_int, P(ctypes.c_int),
+                                             ctypes.c_size_t, P(ctypes.c_size_t)]
+    lib.emprise_tokenizer_decode.restype = ctypes.c_int
+    lib.emprise_tokenizer_decode.argtypes = [vp, ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t, P(ctypes.c_size_t)]
+    lib.emprise_tokenizer_chat_prompt.restype = ctypes.c_int
+    lib.emprise_tokenizer_chat_prompt.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p,
+                                                  ctypes.c_size_t, P(ctypes.c_size_t)]
     lib.emprise_model_last_hidden_normed.restype = ctypes.c_int
     lib.emprise_model_last_hidden_normed.argtypes = [vp, P(ctypes.c_float)]
     lib.emprise_model_evaluate_block.restype = ctypes.c_int
@@ -490,11 +504,63 @@ def _host_check(status: int):
         raise EmpriseError(status, msg)
 
 
-def synth_write(path, seed: int = 0, matrix_type: int = Q6_K, q4_k_m_mix: bool = False, mtp: bool = False, **shape):
+def synth_write(path, seed: int = 0, matrix_type: int = Q6_K, q4_k_m_mix: bool = False, mtp: bool = False,
+                tokenizer: bool = False, **shape):
     """Writes a deterministic synthetic qwen35 GGUF (see emprise_synth_write); mtp adds the
-    next-n block blk.<layers>."""
-    c = SynthConfig(seed=seed, matrix_type=matrix_type, q4_k_m_mix=int(q4_k_m_mix), mtp=int(mtp), **shape)
+    next-n block blk.<layers>, tokenizer a qwen35 GPT-2 BPE tokenizer."""
+    c = SynthConfig(seed=seed, matrix_type=matrix_type, q4_k_m_mix=int(q4_k_m_mix), mtp=int(mtp),
+                    tokenizer=int(tokenizer), **shape)
     _host_check(host_lib().emprise_synth_write(ctypes.byref(c), str(path).encode()))
+
+
+class Tokenizer:
+    """The qwen35 GPT-2 BPE tokenizer of a GGUF file (emprise_tokenizer_*; reference
+    include/emprise/tokenizer.hpp). Tokenizer(path) reads the file's metadata without a
+    device; Model.tokenizer is the model's own."""
+
+    def __init__(self, path=None, _handle=None, _owner=None):
+        if _handle is not None:
+            self.t, self._owned, self._owner = _handle, False, _owner
+        else:
+            h = ctypes.c_void_p()
+            _host_check(host_lib().emprise_tokenizer_open(str(path).encode(), ctypes.byref(h)))
+            self.t, self._owned, self._owner = h, True, None
+
+    def encode(self, text: str, parse_special: bool = True) -> list:
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        n = ctypes.c_size_t()
+        _host_check(host_lib().emprise_tokenizer_encode(self.t, b, len(b), int(parse_special), None, 0,
+                                                        ctypes.byref(n)))
+        ids = (ctypes.c_int * max(n.value, 1))()
+        _host_check(host_lib().emprise_tokenizer_encode(self.t, b, len(b), int(parse_special), ids, n.value,
+                                                        ctypes.byref(n)))
+        return list(ids[:n.value])
+
+    def decode(self, token: int) -> bytes:
+        n = ctypes.c_size_t()
+        _host_check(host_lib().emprise_tokenizer_decode(self.t, token, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(max(n.value, 1))
+        _host_check(host_lib().emprise_tokenizer_decode(self.t, token, buf, n.value, ctypes.byref(n)))
+        return buf.raw[:n.value]
+
+    def chat_prompt(self, user: str) -> str:
+        b = user.encode()
+        n = ctypes.c_size_t()
+        _host_check(host_lib().emprise_tokenizer_chat_prompt(self.t, b, len(b), None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(max(n.value, 1))
+        _host_check(host_lib().emprise_tokenizer_chat_prompt(self.t, b, len(b), buf, n.value, ctypes.byref(n)))
+        return buf.raw[:n.value].decode()
+
+    def close(self):
+        if self._owned and self.t:
+            host_lib().emprise_tokenizer_close(self.t)
+        self.t = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 def gguf_inspect(path):
@@ -586,6 +652,12 @@ class Model:
     @property
     def has_mtp(self) -> bool:
         return bool(host_lib().emprise_model_has_mtp(self.m))
+
+    @property
+    def tokenizer(self):
+        """The model's tokenizer (Model::tokenizer), or None when the file has none."""
+        h = host_lib().emprise_model_tokenizer(self.m)
+        return Tokenizer(_handle=ctypes.c_void_p(h), _owner=self) if h else None
 
     def mtp_draft(self, hidden, token: int, position: int) -> np.ndarray:
         """Model::mtp_draft: the MTP head's logits for the token after `token`."""

@@ -9,15 +9,25 @@
 #include "emprise_host.h"
 #include "gguf.hpp"
 #include "model.hpp"
+#include "tokenizer.hpp"
 
 namespace emprise {
 void synth_write(const emprise_synth_config& c, const std::string& path);
 void synth_prompt(uint64_t seed, int vocab, size_t n, int* ids);
 }  // namespace emprise
 
+// A tokenizer handle: one opened from a file (owning the GGUF mapping) or the view of a
+// model's own tokenizer.
+struct emprise_tokenizer {
+    std::unique_ptr<emprise::Gguf> file;
+    std::unique_ptr<emprise::Tokenizer> owned;
+    const emprise::Tokenizer* tok = nullptr;
+};
+
 struct emprise_model {
     std::unique_ptr<emprise::Model> model;
     std::string name;
+    emprise_tokenizer tokenizer;
 };
 
 namespace {
@@ -39,6 +49,20 @@ template <class F> emprise_status guarded(F&& f) {
     } catch (const std::exception& e) {
         g_error = e.what();
         return EMPRISE_EDEVICE;
+    }
+}
+// Tokenizer calls fail only on their input (invalid UTF-8, an unknown id) or on the
+// file's vocabulary: every error is EINVAL.
+template <class F> emprise_status guarded_input(F&& f) {
+    try {
+        f();
+        return EMPRISE_OK;
+    } catch (const std::bad_alloc&) {
+        g_error = "out of host memory";
+        return EMPRISE_ENOMEM;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return EMPRISE_EINVAL;
     }
 }
 }  // namespace
@@ -83,7 +107,73 @@ emprise_status emprise_model_open(const emprise_model_options* o, emprise_model*
         auto m = std::make_unique<emprise_model>();
         m->model = std::make_unique<emprise::Model>(opt);
         m->name = m->model->backend_name();
+        m->tokenizer.tok = m->model->tokenizer();
         *out = m.release();
+    });
+}
+
+const emprise_tokenizer* emprise_model_tokenizer(const emprise_model* m) {
+    return m && m->tokenizer.tok ? &m->tokenizer : nullptr;
+}
+
+emprise_status emprise_tokenizer_open(const char* path, emprise_tokenizer** out) {
+    if (!path || !out) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    *out = nullptr;
+    return guarded([&] {
+        auto t = std::make_unique<emprise_tokenizer>();
+        t->file = std::make_unique<emprise::Gguf>(path);
+        try {
+            t->owned = std::make_unique<emprise::Tokenizer>(*t->file);
+        } catch (const std::runtime_error& e) {
+            throw std::invalid_argument(e.what());  // a file without a usable tokenizer
+        }
+        t->tok = t->owned.get();
+        *out = t.release();
+    });
+}
+
+void emprise_tokenizer_close(emprise_tokenizer* t) {
+    if (t && t->owned) delete t;  // a model's view is owned by the model
+}
+
+emprise_status emprise_tokenizer_encode(const emprise_tokenizer* t, const char* text, size_t len, int parse_special,
+                                        int* ids, size_t cap, size_t* n) {
+    if (!t || !t->tok || (!text && len) || (!ids && cap) || !n) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded_input([&] {
+        const auto v = t->tok->encode(std::string(text ? text : "", len), parse_special != 0);
+        std::copy(v.begin(), v.begin() + static_cast<std::ptrdiff_t>(std::min(cap, v.size())), ids);
+        *n = v.size();
+    });
+}
+
+emprise_status emprise_tokenizer_decode(const emprise_tokenizer* t, int token, char* out, size_t cap, size_t* n) {
+    if (!t || !t->tok || (!out && cap) || !n) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded_input([&] {
+        const std::string s = t->tok->decode(token);
+        std::memcpy(out, s.data(), std::min(cap, s.size()));
+        *n = s.size();
+    });
+}
+
+emprise_status emprise_tokenizer_chat_prompt(const emprise_tokenizer* t, const char* user, size_t len, char* out,
+                                             size_t cap, size_t* n) {
+    if (!t || !t->tok || (!user && len) || (!out && cap) || !n) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded_input([&] {
+        const std::string s = t->tok->chat_prompt(std::string(user ? user : "", len));
+        std::memcpy(out, s.data(), std::min(cap, s.size()));
+        *n = s.size();
     });
 }
 

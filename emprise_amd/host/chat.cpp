@@ -1,12 +1,15 @@
 // emprise-chat for the HIP backend (reference src/chat.cpp): loads a qwen35 GGUF,
-// greedy-decodes from token ids, prints timings, writes the --report JSON with the
-// reference's fields plus the weight-bytes roofline. Text tokenisation is outside
-// this build, so prompts are token ids (--prompt-ids or a seeded --synthetic-prompt).
+// greedy-decodes from a text prompt (--prompt / --prompt-file, through the file's
+// tokenizer and chat template unless --raw), token ids (--prompt-ids) or a seeded
+// --synthetic-prompt, prints the output and timings, writes the --report JSON with the
+// reference's fields plus the weight-bytes roofline. --tokenize prints the prompt's ids
+// without touching the device (chat.cpp:47-52).
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <fstream>
 #include <iostream>
+#include <iterator>
 #include <sstream>
 #include <stdexcept>
 #include <string>
@@ -30,22 +33,81 @@ std::vector<int> parse_ids(const std::string& s) {
     return ids;
 }
 
-// A JSON string literal: quotes, backslashes and control characters escaped.
+// Length of the well-formed UTF-8 sequence at s[i], or 0.
+size_t utf8_length(const std::string& s, size_t i) {
+    const auto b = [&](size_t k) { return static_cast<unsigned char>(s[k]); };
+    const unsigned char c = b(i);
+    size_t n;
+    uint32_t cp;
+    if (c < 0x80) return 1;
+    if ((c & 0xE0) == 0xC0) n = 2, cp = c & 0x1F;
+    else if ((c & 0xF0) == 0xE0) n = 3, cp = c & 0x0F;
+    else if ((c & 0xF8) == 0xF0) n = 4, cp = c & 0x07;
+    else return 0;
+    if (i + n > s.size()) return 0;
+    for (size_t k = 1; k < n; ++k) {
+        if ((b(i + k) & 0xC0) != 0x80) return 0;
+        cp = (cp << 6) | (b(i + k) & 0x3F);
+    }
+    const uint32_t min = n == 2 ? 0x80 : n == 3 ? 0x800 : 0x10000;
+    if (cp < min || cp > 0x10FFFF || (cp >= 0xD800 && cp <= 0xDFFF)) return 0;
+    return n;
+}
+
+// A JSON string literal: quotes, backslashes and control characters escaped, and each
+// byte that is not part of well-formed UTF-8 replaced by U+FFFD (the reference writes
+// its report with nlohmann::json's error_handler_t::replace, chat.cpp:85).
 std::string json_string(const std::string& s) {
     std::string o = "\"";
-    for (unsigned char c : s) {
-        if (c == '"' || c == '\\') {
+    for (size_t i = 0; i < s.size();) {
+        const unsigned char c = static_cast<unsigned char>(s[i]);
+        const size_t n = utf8_length(s, i);
+        if (!n) {
+            o += "\xEF\xBF\xBD";
+            ++i;
+        } else if (c == '"' || c == '\\') {
             o += '\\';
             o += static_cast<char>(c);
+            ++i;
         } else if (c < 0x20) {
             char buf[8];
             std::snprintf(buf, sizeof buf, "\\u%04x", c);
             o += buf;
+            ++i;
         } else {
-            o += static_cast<char>(c);
+            o.append(s, i, n);
+            i += n;
         }
     }
     return o + "\"";
+}
+
+// The tokenizer's text as a std::string, or an exception with the library's message.
+std::string take_string(emprise_status st, const std::vector<char>& buf, size_t n) {
+    check(st);
+    return std::string(buf.data(), n);
+}
+
+std::vector<int> encode(const emprise_tokenizer* t, const std::string& text) {
+    size_t n = 0;
+    check(emprise_tokenizer_encode(t, text.data(), text.size(), 1, nullptr, 0, &n));
+    std::vector<int> ids(n);
+    check(emprise_tokenizer_encode(t, text.data(), text.size(), 1, ids.data(), ids.size(), &n));
+    return ids;
+}
+
+std::string chat_prompt(const emprise_tokenizer* t, const std::string& user) {
+    size_t n = 0;
+    check(emprise_tokenizer_chat_prompt(t, user.data(), user.size(), nullptr, 0, &n));
+    std::vector<char> buf(n + 1);
+    return take_string(emprise_tokenizer_chat_prompt(t, user.data(), user.size(), buf.data(), buf.size(), &n), buf, n);
+}
+
+std::string decode(const emprise_tokenizer* t, int id) {
+    size_t n = 0;
+    check(emprise_tokenizer_decode(t, id, nullptr, 0, &n));
+    std::vector<char> buf(n + 1);
+    return take_string(emprise_tokenizer_decode(t, id, buf.data(), buf.size(), &n), buf, n);
 }
 
 template <class T> std::string json_list(const std::vector<T>& v) {
@@ -60,7 +122,8 @@ template <class T> std::string json_list(const std::vector<T>& v) {
 
 int main(int argc, char** argv) {
     try {
-        std::string model, report_file, ids;
+        std::string model, report_file, ids, text, prompt_file;
+        bool have_text = false, raw = false, tokenize = false;
         size_t count = 32, synthetic = 0;
         uint64_t seed = 0;
         emprise_model_options opt{};
@@ -74,6 +137,10 @@ int main(int argc, char** argv) {
                 return std::string(argv[++i]);
             };
             if (arg == "--model") model = value();
+            else if (arg == "--prompt") text = value(), have_text = true;
+            else if (arg == "--prompt-file") prompt_file = value(), have_text = true;
+            else if (arg == "--raw") raw = true;
+            else if (arg == "--tokenize") tokenize = true;
             else if (arg == "--prompt-ids") ids = value();
             else if (arg == "--synthetic-prompt") synthetic = std::stoull(value());
             else if (arg == "--seed") seed = std::stoull(value());
@@ -91,9 +158,26 @@ int main(int argc, char** argv) {
             else throw std::invalid_argument("Unknown option: " + arg);
         }
         if (model.empty())
-            throw std::invalid_argument("Usage: emprise-chat --model MODEL.gguf (--prompt-ids 1,2,3 | --synthetic-prompt N "
-                                        "[--seed S]) [--tokens N] [--context N] [--fast-q8] [--report FILE] [--unfused] "
+            throw std::invalid_argument("Usage: emprise-chat --model MODEL.gguf (--prompt TEXT | --prompt-file FILE | "
+                                        "--prompt-ids 1,2,3 | --synthetic-prompt N [--seed S]) [--raw] [--tokenize] "
+                                        "[--tokens N] [--context N] [--fast-q8] [--report FILE] [--unfused] "
                                         "[--no-graph] [--no-batch-prefill] [--step-program]");
+        if (!prompt_file.empty()) {
+            std::ifstream f(prompt_file, std::ios::binary);
+            if (!f) throw std::runtime_error("Cannot read prompt");
+            text.assign(std::istreambuf_iterator<char>(f), {});
+        }
+        if (tokenize) {
+            // the file's tokenizer alone, no device (chat.cpp:47-52)
+            emprise_tokenizer* t = nullptr;
+            check(emprise_tokenizer_open(model.c_str(), &t));
+            const auto toks = encode(t, raw ? text : chat_prompt(t, text));
+            emprise_tokenizer_close(t);
+            std::cout << '[';
+            for (size_t i = 0; i < toks.size(); ++i) std::cout << (i ? "," : "") << toks[i];
+            std::cout << "]\n";
+            return 0;
+        }
         opt.path = model.c_str();
         const auto start = std::chrono::steady_clock::now();
         emprise_model* m = nullptr;
@@ -101,7 +185,12 @@ int main(int argc, char** argv) {
         emprise_model_info info{};
         check(emprise_model_get_info(m, &info));
         std::cerr << "Backend: " << emprise_model_backend_name(m) << '\n';
+        const emprise_tokenizer* tok = emprise_model_tokenizer(m);
         std::vector<int> prompt = parse_ids(ids);
+        if (have_text) {
+            if (!tok) throw std::runtime_error("The model file has no qwen35 GPT-2 BPE tokenizer");
+            prompt = encode(tok, raw ? text : chat_prompt(tok, text));
+        }
         if (synthetic) {
             prompt.resize(synthetic);
             check(emprise_synth_prompt(seed, info.vocab, synthetic, prompt.data()));
@@ -113,8 +202,14 @@ int main(int argc, char** argv) {
         check(emprise_model_generate(m, prompt.data(), prompt.size(), count, tokens.data(), &emitted, arrivals.data()));
         tokens.resize(emitted);
         arrivals.resize(emitted);
-        for (size_t i = 0; i < emitted; ++i) std::cout << (i ? " " : "") << tokens[i];
-        std::cout << '\n';
+        std::string output_text;
+        if (tok) {
+            for (size_t i = 0; i < emitted; ++i) output_text += decode(tok, tokens[i]);
+            std::cout << output_text << '\n';
+        } else {
+            for (size_t i = 0; i < emitted; ++i) std::cout << (i ? " " : "") << tokens[i];
+            std::cout << '\n';
+        }
         const double load = std::chrono::duration<double>(loaded - start).count();
         const double first = emitted ? arrivals.front() : 0.0;
         const double rate = emitted > 1 ? double(emitted - 1) / (arrivals.back() - arrivals.front()) : 0.0;
@@ -123,7 +218,7 @@ int main(int argc, char** argv) {
                   << "; decode: " << rate << " tokens/s (" << 100.0 * roofline << "% of the 8 TB/s weight roofline)\n";
         if (!report_file.empty()) {
             // The reference's --report fields (chat.cpp:77-84), then this build's roofline.
-            // text: token ids are not detokenised here. matrix_seconds / matrix_calls /
+            // text: the decoded output ("" without a tokenizer). matrix_seconds / matrix_calls /
             // non_matrix_seconds are the reference's host timers around each backend call;
             // the device path replays one graph per token and has no such calls: 0.
             std::ofstream f(report_file);
@@ -131,7 +226,8 @@ int main(int argc, char** argv) {
             f.precision(9);
             f << "{\n  \"engine\": \"emprise mi355x\",\n  \"backend\": " << json_string(emprise_model_backend_name(m))
               << ",\n  \"model\": " << json_string(model) << ",\n  \"prompt_tokens\": " << json_list(prompt)
-              << ",\n  \"output_tokens\": " << json_list(tokens) << ",\n  \"text\": \"\",\n  \"load_seconds\": " << load
+              << ",\n  \"output_tokens\": " << json_list(tokens) << ",\n  \"text\": " << json_string(output_text)
+              << ",\n  \"load_seconds\": " << load
               << ",\n  \"first_token_seconds\": " << first << ",\n  \"generation_tokens_per_second\": " << rate
               << ",\n  \"content_arrivals_seconds\": " << json_list(arrivals)
               << ",\n  \"matrix_seconds\": 0,\n  \"matrix_calls\": 0,\n  \"non_matrix_seconds\": 0"

@@ -62,9 +62,19 @@ public:
             const auto sub = scalar<uint32_t>();
             const auto count = scalar<uint64_t>();
             if (count > size_ - pos_) throw std::runtime_error("GGUF: a metadata array longer than the file");
-            for (uint64_t i = 0; i < count; ++i) (void)value(sub, depth + 1);
+            // string and integer arrays are kept (the tokenizer's vocabulary, merges and
+            // token types); others are validated and skipped
+            const bool integer = sub <= 5 || sub == 10 || sub == 11;
+            if (sub == 8) v.strings.reserve(count);
+            if (integer) v.integers.reserve(count);
+            for (uint64_t i = 0; i < count; ++i) {
+                MetaValue e = value(sub, depth + 1);
+                if (sub == 8) v.strings.push_back(std::move(e.text));
+                else if (integer) v.integers.push_back(static_cast<int64_t>(e.number));
+            }
             v.is_array = true;
             v.array_len = count;
+            v.array_type = sub;
             break;
         }
         case 10: v.number = (double)scalar<uint64_t>(); break;

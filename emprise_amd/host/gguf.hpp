@@ -25,6 +25,9 @@ struct MetaValue {
     std::string text;   // strings
     uint64_t array_len = 0;
     bool is_array = false;
+    uint32_t array_type = 0;           // element type of an array
+    std::vector<std::string> strings;  // elements of a string array
+    std::vector<int64_t> integers;     // elements of an integer array
 };
 
 uint64_t encoded_bytes(WeightType type, uint64_t elements);  // the reference's gguf.cpp:72-85 (throws)

@@ -64,6 +64,11 @@ Model::Model(const ModelOptions& options) : opt_(options) {
     const Gguf& g = *gguf_;
     const MetaValue* arch = g.meta("general.architecture");
     if (!arch || arch->text != "qwen35") throw std::runtime_error("Only qwen35 is implemented");
+    try {
+        tokenizer_ = std::make_unique<Tokenizer>(g);
+    } catch (const std::exception& e) {
+        tokenizer_error_ = e.what();  // token ids still work; text calls report this
+    }
     auto integer = [&](const char* key) { return g.meta_int(std::string("qwen35.") + key); };
     emprise_model_info& d = info_;
     d.hidden = integer("embedding_length");

@@ -11,6 +11,7 @@
 #include "emprise_host.h"
 #include "gguf.hpp"
 #include "hip_backend.hpp"
+#include "tokenizer.hpp"
 
 namespace emprise {
 
@@ -36,6 +37,10 @@ public:
     Model& operator=(const Model&) = delete;
 
     std::string backend_name() const { return backend_->name(); }
+    // Model::tokenizer (model.hpp:33): null when the file has no qwen35 GPT-2 BPE
+    // tokenizer (tokenizer_error() says why); the reference requires one to load
+    const Tokenizer* tokenizer() const { return tokenizer_.get(); }
+    const std::string& tokenizer_error() const { return tokenizer_error_; }
     emprise_model_info info() const { return info_; }
     void reset();
     std::vector<float> evaluate(int token, bool want_logits = true);
@@ -78,6 +83,8 @@ private:
 
     ModelOptions opt_;
     std::unique_ptr<Gguf> gguf_;
+    std::unique_ptr<Tokenizer> tokenizer_;
+    std::string tokenizer_error_;
     std::unique_ptr<HipBackend> backend_;
     emprise_model_info info_{};
     std::vector<Layer> layers_;

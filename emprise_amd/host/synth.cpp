@@ -3,14 +3,17 @@
 // Every tensor draws from its own counter-based SplitMix64 stream, keyed by the seed
 // and the tensor name, so the bytes are the same for any thread count or host.
 // Normals are Irwin-Hall sums of twelve 16-bit uniforms (IEEE adds only).
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "emprise_host.h"
+#include "tokenizer.hpp"
 
 namespace emprise {
 
@@ -143,6 +146,88 @@ void fill(const TensorSpec& t, uint64_t seed, uint8_t* out) {
     }
 }
 
+// The synthetic tokenizer: GPT-2's byte encoder strings for the 256 bytes, then the
+// merges of a byte-pair training run on kCorpus (the most frequent adjacent pair over
+// the pre-tokenizer's pieces, ties to the smaller pair string), then the chat template's
+// special tokens, then numbered control tokens up to `vocab`.
+const char* const kCorpus =
+    "The quick brown fox jumps over the lazy dog. The dog sleeps; the fox runs away!\n"
+    "Explain how a refrigerator works. A refrigerator moves heat from the inside to the "
+    "outside: the compressor squeezes the refrigerant, which gets hot, and the coils let "
+    "the heat go. It's cold inside because the liquid evaporates and takes heat with it.\n"
+    "In 2024 there were 365 days, 12 months and 52 weeks; 3.14159 is pi, 2.71828 is e.\n"
+    "    def add(a, b):\n        return a + b  # they'll add, we've seen it, I'd say\n"
+    "Grüße aus München! Ça va? Numbers: 0 1 2 3 4 5 6 7 8 9, 10 100 1000.\n\n";
+const char* const kSpecials[] = {"<|endoftext|>", "<|im_start|>", "<|im_end|>", "<think>", "</think>"};
+
+struct SynthVocab {
+    std::vector<std::string> tokens, merges;
+    std::vector<int32_t> types;
+};
+
+SynthVocab synth_vocab(int vocab) {
+    SynthVocab v;
+    std::string enc[256];
+    int extra = 256;
+    for (int b = 0; b < 256; ++b) {
+        const bool direct = (b >= 33 && b <= 126) || (b >= 161 && b <= 172) || b >= 174;
+        const uint32_t c = direct ? static_cast<uint32_t>(b) : static_cast<uint32_t>(extra++);
+        enc[b] = c < 0x80 ? std::string(1, static_cast<char>(c))
+                          : std::string{static_cast<char>(0xC0 | (c >> 6)), static_cast<char>(0x80 | (c & 0x3F))};
+        v.tokens.push_back(enc[b]);
+        v.types.push_back(1);
+    }
+    // words of the corpus as sequences of byte-encoded symbols, with their counts
+    const std::string text = kCorpus;
+    std::map<std::vector<std::string>, int> words;
+    size_t start = 0;
+    for (size_t end : pretokenize(text)) {
+        std::vector<std::string> w;
+        for (size_t i = start; i < end; ++i) w.push_back(enc[static_cast<uint8_t>(text[i])]);
+        ++words[w];
+        start = end;
+    }
+    const int specials = static_cast<int>(sizeof kSpecials / sizeof kSpecials[0]);
+    const int budget = std::min(400, vocab - 256 - specials);
+    for (int m = 0; m < budget; ++m) {
+        std::map<std::pair<std::string, std::string>, int> freq;
+        for (const auto& [w, n] : words)
+            for (size_t i = 0; i + 1 < w.size(); ++i) freq[{w[i], w[i + 1]}] += n;
+        if (freq.empty()) break;
+        auto best = freq.begin();
+        for (auto it = freq.begin(); it != freq.end(); ++it)
+            if (it->second > best->second) best = it;  // map order: ties keep the smaller pair
+        const auto [a, b] = best->first;
+        v.merges.push_back(a + " " + b);
+        v.tokens.push_back(a + b);
+        v.types.push_back(1);
+        std::map<std::vector<std::string>, int> next;
+        for (const auto& [w, n] : words) {
+            std::vector<std::string> r;
+            for (size_t i = 0; i < w.size(); ++i) {
+                if (i + 1 < w.size() && w[i] == a && w[i + 1] == b) {
+                    r.push_back(a + b);
+                    ++i;
+                } else {
+                    r.push_back(w[i]);
+                }
+            }
+            next[r] += n;
+        }
+        words.swap(next);
+    }
+    for (const char* sp : kSpecials) {
+        v.tokens.push_back(sp);
+        v.types.push_back(3);
+    }
+    for (int i = 0; static_cast<int>(v.tokens.size()) < vocab; ++i) {
+        v.tokens.push_back("<|control_" + std::to_string(i) + "|>");
+        v.types.push_back(3);
+    }
+    if (static_cast<int>(v.tokens.size()) != vocab) throw std::invalid_argument("synthetic vocabulary too small");
+    return v;
+}
+
 struct Writer {
     FILE* f;
     void raw(const void* p, size_t n) {
@@ -172,6 +257,20 @@ struct Writer {
         str(k);
         put<uint32_t>(10);
         put<uint64_t>(v);
+    }
+    void kv_strings(const std::string& k, const std::vector<std::string>& v) {
+        str(k);
+        put<uint32_t>(9);
+        put<uint32_t>(8);
+        put<uint64_t>(v.size());
+        for (const auto& e : v) str(e);
+    }
+    void kv_i32s(const std::string& k, const std::vector<int32_t>& v) {
+        str(k);
+        put<uint32_t>(9);
+        put<uint32_t>(5);
+        put<uint64_t>(v.size());
+        for (int32_t e : v) put<int32_t>(e);
     }
 };
 
@@ -253,7 +352,9 @@ void synth_write(const emprise_synth_config& c, const std::string& path) {
     if (!f) throw std::runtime_error("Cannot write " + path);
     Writer w{f};
     try {
-        const int kv_count = 22 + (c.mtp ? 1 : 0);
+        SynthVocab sv;
+        if (c.tokenizer) sv = synth_vocab(c.vocab);
+        const int kv_count = 22 + (c.mtp ? 1 : 0) + (c.tokenizer ? 4 : 0);
         w.put<uint32_t>(0x46554747u);
         w.put<uint32_t>(3);
         w.put<uint64_t>(ts.size());
@@ -280,7 +381,15 @@ void synth_write(const emprise_synth_config& c, const std::string& path) {
         w.kv_u32("qwen35.ssm.inner_size", static_cast<uint32_t>(vd));
         w.kv_u32("qwen35.full_attention_interval", static_cast<uint32_t>(c.full_attention_interval));
         w.kv_u32("tokenizer.ggml.eos_token_id", static_cast<uint32_t>(c.eos));
-        w.kv_str("tokenizer.ggml.model", "none");
+        if (c.tokenizer) {
+            w.kv_str("tokenizer.ggml.model", "gpt2");
+            w.kv_str("tokenizer.ggml.pre", "qwen35");
+            w.kv_strings("tokenizer.ggml.tokens", sv.tokens);
+            w.kv_i32s("tokenizer.ggml.token_type", sv.types);
+            w.kv_strings("tokenizer.ggml.merges", sv.merges);
+        } else {
+            w.kv_str("tokenizer.ggml.model", "none");
+        }
         for (const auto& t : ts) {
             w.str(t.name);
             w.put<uint32_t>(static_cast<uint32_t>(t.shape.size()));

@@ -111,6 +111,27 @@ emprise_status emprise_model_generate(emprise_model* m, const int* prompt, size_
 emprise_status emprise_model_trace_step(emprise_model* m, int token, emprise_hip_trace_record* records, size_t cap,
                                         size_t* n);
 
+/* ---- tokenizer (include/emprise/tokenizer.hpp, src/tokenizer.cpp) ----------------- */
+/* The qwen35 GPT-2 byte-level BPE of a GGUF's tokenizer.ggml.* metadata. */
+typedef struct emprise_tokenizer emprise_tokenizer;
+/* A file's tokenizer without a device (the reference's --tokenize path, chat.cpp:47-52):
+ * EINVAL when the file has no qwen35 GPT-2 BPE tokenizer (tokenizer.cpp:62-63). */
+emprise_status emprise_tokenizer_open(const char* path, emprise_tokenizer** out);
+/* Releases a tokenizer from emprise_tokenizer_open; a model's tokenizer is left alone. */
+void emprise_tokenizer_close(emprise_tokenizer* t);
+/* Model::tokenizer (model.hpp:33): the model's tokenizer, NULL when its file has none. */
+const emprise_tokenizer* emprise_model_tokenizer(const emprise_model* m);
+/* Tokenizer::encode (tokenizer.cpp:114-131): len bytes of UTF-8 text; parse_special
+ * matches special tokens verbatim. Writes min(cap, count) ids and the count to *n. */
+emprise_status emprise_tokenizer_encode(const emprise_tokenizer* t, const char* text, size_t len, int parse_special,
+                                        int* ids, size_t cap, size_t* n);
+/* Tokenizer::decode (tokenizer.cpp:132-135): the token's bytes (min(cap, count) written,
+ * no terminator; the count in *n). EINVAL for an id outside the vocabulary. */
+emprise_status emprise_tokenizer_decode(const emprise_tokenizer* t, int token, char* out, size_t cap, size_t* n);
+/* Tokenizer::chat_prompt (tokenizer.cpp:136-139): the single-turn template around user. */
+emprise_status emprise_tokenizer_chat_prompt(const emprise_tokenizer* t, const char* user, size_t len, char* out,
+                                             size_t cap, size_t* n);
+
 /* ---- synthetic qwen35 GGUF (test and benchmark inputs) ----------------------- */
 typedef struct {
     uint64_t seed;
@@ -124,6 +145,8 @@ typedef struct {
     uint32_t matrix_type; /* EMPRISE_Q6_K or EMPRISE_Q4_K for every matrix */
     int q4_k_m_mix;       /* 1: attn_v and ffn_down Q6_K, every other matrix Q4_K */
     int mtp;              /* 1: add the MTP (next-n) block blk.<layers> (qwen35.nextn_predict_layers = 1) */
+    int tokenizer;        /* 1: add a qwen35 GPT-2 BPE tokenizer: 256 byte tokens, merges trained on a
+                             built-in text, the chat template's special tokens, control tokens up to vocab */
 } emprise_synth_config;
 
 /* Writes a GGUF v3 file with deterministic weights: counter-based SplitMix64 streams per

@@ -218,3 +218,47 @@ def test_chat_cli_report(tmp_path):
     ref_tokens, margins = oracle.Model(str(model), context=512).generate(prompt, 16)
     assert _greedy_agreement(rep["output_tokens"], ref_tokens, margins) >= 8
     assert r.stdout.split() == [str(t) for t in rep["output_tokens"]]
+
+
+def test_chat_cli_text_prompt(tmp_path):
+    """emprise-chat --prompt TEXT on a tiny model with the synthetic tokenizer: the prompt
+    goes through the chat template and the tokenizer (prompt_tokens are the CPU
+    tokenizer's), the greedy tokens are the oracle's, and the printed text and the
+    report's `text` are the decoded output tokens (chat.cpp:53-75)."""
+    import json
+    import subprocess
+    from pathlib import Path
+    from oracle.tokenizer import Tokenizer as OracleTokenizer
+    exe = Path(__file__).resolve().parent.parent / "emprise_amd" / "emprise-chat"
+    model = tmp_path / "tiny_tok.gguf"
+    synth_write(model, seed=3, tokenizer=True, **TINY)
+    text = "Explain how a refrigerator works."
+    report = tmp_path / "report.json"
+    r = subprocess.run([str(exe), "--model", str(model), "--prompt", text, "--tokens", "12", "--context", "512",
+                        "--report", str(report)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    rep = json.loads(report.read_text())
+    tok = OracleTokenizer.from_file(model)
+    prompt = tok.encode(tok.chat_prompt(text))
+    assert rep["prompt_tokens"] == prompt
+    ref_tokens, margins = oracle.Model(str(model), context=512).generate(prompt, 12)
+    assert _greedy_agreement(rep["output_tokens"], ref_tokens, margins) >= 6
+    raw = b"".join(tok.decode(t) for t in rep["output_tokens"])
+    assert rep["text"] == _replace_bad_utf8(raw)
+
+
+def _replace_bad_utf8(b: bytes) -> str:
+    """The report's rule: well-formed UTF-8 kept, every other byte replaced by U+FFFD."""
+    out, i = [], 0
+    while i < len(b):
+        for n in (1, 2, 3, 4):
+            try:
+                out.append(b[i:i + n].decode("utf-8"))
+                i += n
+                break
+            except UnicodeDecodeError:
+                continue
+        else:
+            out.append("\ufffd")
+            i += 1
+    return "".join(out)
