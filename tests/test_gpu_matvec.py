@@ -390,3 +390,34 @@ def test_lm_head_q8(backend_q8, vocab, hidden):
     for b in (xd, dd, xo, ld, idx):
         be.free(b)
     be.weight_free(w)
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (12288, 4096), (1024, 12288)])
+def test_q8_register_quantiser_matches_lds_pass(backend_q8, rows, cols):
+    """The quantiser in the fused-norm staging (from registers) against the generic
+    staging's LDS pass, bit for bit. The input has mean(v^2) = 1 exactly (5/8 of the
+    entries +-0.5, 3/8 +-1.5, in a seeded order) and the norm weights are 1 with eps = 0,
+    so rms(v) * norm = v exactly and both paths quantise the same floats: once as
+    x = v - delta, delta with the residual add, once as plain v without the norm."""
+    rng = np.random.default_rng(rows * 3 + cols)
+    mag = np.where(np.arange(cols) < cols * 5 // 8, 0.5, 1.5)
+    v = (rng.permutation(mag) * rng.choice([-1.0, 1.0], cols)).astype(np.float32)
+    delta = (rng.integers(-8, 9, cols) * 0.25).astype(np.float32)  # v - delta exact in FP32
+    x = (v - delta).astype(np.float32)
+    assert np.array_equal((x + delta).astype(np.float32), v) and float(np.mean(v.astype(np.float64) ** 2)) == 1.0
+    be = backend_q8
+    raw = matrix(rng, Q6_K, rows, cols)
+    w, ones = be.upload_weight(Q6_K, cols, rows, raw), be.vector(np.ones(cols, np.float32))
+    vd, xd, dd, xo = be.to_device(v), be.to_device(x), be.to_device(delta), be.alloc(cols * 4)
+    y_plain, y_norm, y_delta = be.alloc(rows * 4), be.alloc(rows * 4), be.alloc(rows * 4)
+    be.linear(w, vd, y_plain)
+    be.linear_norm(Input(vd, 0, 0, ones, 0.0), [w], [y_norm])
+    be.linear_norm(Input(xd, dd, xo, ones, 0.0), [w], [y_delta])
+    a, b, c = (be.download(y, rows) for y in (y_plain, y_norm, y_delta))
+    assert np.array_equal(be.download(xo, cols), v)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+    _q8_check(a, raw, rows, cols, v)
+    for t in (vd, xd, dd, xo, y_plain, y_norm, y_delta):
+        be.free(t)
+    be.weight_free(w)
