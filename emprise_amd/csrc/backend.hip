@@ -849,12 +849,30 @@ static emprise_status linear_batch_rows(emprise_hip* h, int nw, const Weight* co
     if (K < kGemmMinBatch || cols % 16 != 0 || X % 16 != 0 || ldx % 4 != 0) {
         uint64_t off = 0;
         for (int i = 0; i < nw; ++i) {
-            for (int k = 0; k < K; ++k) {
-                Proj p{ws[i], reinterpret_cast<float*>(Y) + (size_t)k * ldy + off};
-                TRY(run_matvec(h, &p, 1, kMvPlain, nullptr, reinterpret_cast<const float*>(X) + (size_t)k * ldx,
-                               nullptr, nullptr, 0, nullptr));
+            const Weight* wt = ws[i];
+            // 2..kGemmMinBatch-1 rows through a chunked Q6_K/Q4_K matrix: up to kBatchMax rows
+            // per launch, the weights read once per launch (--fast-q8 keeps Q6_K on the
+            // single-input path, which quantises its input)
+            const bool batched = K > 1 && (wt->type == kQ6K || wt->type == kQ4K) && chunked_cols(wt->cols) &&
+                                 !(h->q8 && wt->type == kQ6K) && X % 16 == 0 && ldx % 4 == 0;
+            int per = kBatchMax;
+            while (per > 1 && matvec_batch_lds_bytes(wt->type, cols, per) > kBatchLdsMax) --per;
+            for (int k0 = 0; k0 < K;) {
+                const int n = batched ? std::min(per, K - k0) : 1;
+                float* yk = reinterpret_cast<float*>(Y) + (size_t)k0 * ldy + off;
+                const float* xk = reinterpret_cast<const float*>(X) + (size_t)k0 * ldx;
+                if (n > 1) {
+                    MvBatchArgs b{static_cast<const uint8_t*>(wt->dev), (int)wt->rows, cols, xk, (size_t)ldx, yk,
+                                  (size_t)ldy};
+                    TRY(traced(h, "matvec_batch", wt->bytes + (uint64_t)n * cols * 4,
+                               [&] { return launch_matvec_batch(wt->type, b, n, h->stream); }));
+                } else {
+                    Proj p{wt, yk};
+                    TRY(run_matvec(h, &p, 1, kMvPlain, nullptr, xk, nullptr, nullptr, 0, nullptr));
+                }
+                k0 += n;
             }
-            off += ws[i]->rows;
+            off += wt->rows;
         }
         return EMPRISE_OK;
     }

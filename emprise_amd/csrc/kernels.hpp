@@ -72,6 +72,20 @@ struct MvArgs {
 };
 
 size_t matvec_lds_bytes(uint32_t type, int cols, bool q8);
+// y[k * ldy + r] = row r of w . x[k * ldx ...] for k < K, a chunked Q6_K/Q4_K matrix read
+// once for all K inputs (matvec_batch_kernel)
+struct MvBatchArgs {
+    const uint8_t* w;
+    int rows, cols;
+    const float* x;
+    size_t ldx;
+    float* y;
+    size_t ldy;
+};
+constexpr int kBatchMax = 4;                    // inputs per batched launch
+constexpr size_t kBatchLdsMax = 160 * 1024;     // LDS of one workgroup (one per CU)
+size_t matvec_batch_lds_bytes(uint32_t type, int cols, int k);
+hipError_t launch_matvec_batch(uint32_t type, const MvBatchArgs& a, int k, hipStream_t stream);
 // rows each row-group of MvArgs covers for this weight shape, mode and the launch's
 // total output rows (small launches use one row per wave to spread their arithmetic)
 int matvec_rows_per_group(uint32_t type, uint64_t cols, int mode, uint64_t total_rows);

@@ -1060,9 +1060,110 @@ __global__ __launch_bounds__(256) void dequant_rows_1k_kernel(const uint8_t* w, 
     *reinterpret_cast<float4*>(out + (size_t)r * cols + k) = v;
 }
 
+// ---- small batches: K inputs through one chunked matrix, its weights read once ----------
+//
+// linear_batch for 2 <= K <= kBatchMax rows of X (the reference's chunked prefill and
+// draft verification batch up to 4 positions, cuda.cpp:350-413, model.cpp:355-366). A
+// wave takes whole rows (rows v, v + waves, ...), loads each 4096-column chunk of its row
+// once -- the next chunk's loads in flight while the current one is computed -- and runs
+// the single-input arithmetic (scompute) on it once per staged input, so the K outputs of
+// a row are K single-input dot products over the same weight registers. The inputs sit
+// in LDS side by side, each in the streaming kernels' lane layout with its unit sums;
+// one 16-wave workgroup per CU.
+constexpr int kBatchWaves = 16;
+
+template <int T, int K>
+__global__ __launch_bounds__(kBatchWaves * 64) void matvec_batch_kernel(MvBatchArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int UW = Fmt<T>::unit, U4 = UW / 4;
+    const int cols = a.cols, units = cols / UW, n4 = cols / 4, cpr = cols / kChunkCols;
+    float* xs = reinterpret_cast<float*>(smem);
+    float* usum = xs + (size_t)K * cols;
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const float4* x4 = reinterpret_cast<const float4*>(a.x + (size_t)k * a.ldx);
+        for (int i = threadIdx.x; i < n4; i += blockDim.x) xs4[(size_t)k * n4 + chunk_slot(i)] = x4[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        for (int u = threadIdx.x; u < units; u += blockDim.x) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < U4; ++j) {
+                const float4 v = xs4[(size_t)k * n4 + chunk_slot(u * U4 + j)];
+                sum += (v.x + v.y) + (v.z + v.w);
+            }
+            usum[(size_t)k * units + u] = stored_unit_sum<UW>(sum);
+        }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int waves = gridDim.x * kBatchWaves;
+    const size_t row_bytes = (size_t)(cols / 256) * Fmt<T>::block;
+    for (int row = blockIdx.x * kBatchWaves + wave; row < a.rows; row += waves) {
+        const uint8_t* rp[1] = {a.w + (size_t)row * row_bytes};
+        float acc[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc[k] = 0.f;
+        SChunk<T, 1> cur, next;
+        sload<T, 1>(cur, rp, 0, lane);
+        for (int c = 0; c < cpr; ++c) {
+            if (c + 1 < cpr) sload<T, 1>(next, rp, c + 1, lane);
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                float one[1] = {acc[k]};
+                scompute<T, 1>(cur, one, xs + (size_t)k * cols, usum + (size_t)k * units, c, lane);
+                acc[k] = one[0];
+            }
+            cur = next;
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc[k] = wave_sum(acc[k]);
+        if (lane == 0)
+#pragma unroll
+            for (int k = 0; k < K; ++k) a.y[(size_t)k * a.ldy + row] = acc[k];
+    }
+}
+
 }  // namespace
 
 // ---- host launchers ------------------------------------------------------------------
+
+size_t matvec_batch_lds_bytes(uint32_t type, int cols, int k) {
+    const int unit = type == kQ6K ? 16 : 32;
+    return (size_t)k * ((size_t)cols * 4 + (size_t)(cols / unit) * 4);
+}
+
+template <int T, int K> hipError_t launch_batch_k(const MvBatchArgs& a, size_t lds, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(matvec_batch_kernel<T, K>);
+    const int cap = resident_blocks(fn, lds, kBatchWaves);
+    int blocks = (a.rows + kBatchWaves - 1) / kBatchWaves;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    launch_kernel(matvec_batch_kernel<T, K>, dim3(blocks), dim3(kBatchWaves * 64), lds, stream, a);
+    return hipGetLastError();
+}
+
+template <int T> hipError_t launch_batch_t(const MvBatchArgs& a, int k, size_t lds, hipStream_t stream) {
+    switch (k) {
+    case 1: return launch_batch_k<T, 1>(a, lds, stream);
+    case 2: return launch_batch_k<T, 2>(a, lds, stream);
+    case 3: return launch_batch_k<T, 3>(a, lds, stream);
+    case 4: return launch_batch_k<T, 4>(a, lds, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_matvec_batch(uint32_t type, const MvBatchArgs& a, int k, hipStream_t stream) {
+    if ((type != kQ6K && type != kQ4K) || a.cols % kChunkCols || k < 1 || k > kBatchMax || a.ldx % 4 ||
+        reinterpret_cast<uintptr_t>(a.x) % 16)
+        return hipErrorInvalidValue;
+    const size_t lds = matvec_batch_lds_bytes(type, a.cols, k);
+    if (lds > kBatchLdsMax) return hipErrorInvalidValue;
+    return type == kQ6K ? launch_batch_t<kQ6K>(a, k, lds, stream) : launch_batch_t<kQ4K>(a, k, lds, stream);
+}
 
 size_t matvec_lds_bytes(uint32_t type, int cols, bool q8) {
     if (type == kQ6K || type == kQ4K) {

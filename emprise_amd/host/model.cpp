@@ -495,9 +495,8 @@ std::vector<float> Model::mtp_hidden() {
     return h;
 }
 
-// Every position's logits, positions evaluated in order as decode steps (the reference
-// batches the projections of the block, model.cpp:274-354; per position the arithmetic is
-// the same, so the logits agree up to summation order).
+// Every position's logits (Model::evaluate_block, model.cpp:274-354, which batches the
+// block's projections the same way); a single token is a decode step.
 std::vector<std::vector<float>> Model::evaluate_block(const std::vector<int>& tokens) {
     if (tokens.empty()) throw std::invalid_argument("Empty block");
     if (tokens.size() > opt_.context - std::min(position_, opt_.context))
@@ -505,8 +504,23 @@ std::vector<std::vector<float>> Model::evaluate_block(const std::vector<int>& to
     for (int t : tokens)
         if (t < 0 || t >= info_.vocab) throw std::out_of_range("Token ID");
     std::vector<std::vector<float>> out;
-    out.reserve(tokens.size());
-    for (int t : tokens) out.push_back(evaluate(t, true));
+    if (tokens.size() == 1) {
+        out.push_back(evaluate(tokens[0], true));
+        return out;
+    }
+    // all positions in one batched pass: every projection reads its weights once for the
+    // block (the small-batch matvec up to 7 positions, the GEMM from 8), the recurrent
+    // and attention steps run position by position, then the head over every row
+    const size_t n = tokens.size(), start = position_;
+    backend_->dev_upload(dev_prompt_ + start * sizeof(int), tokens.data(), n * sizeof(int));
+    std::vector<float> flat;
+    prefill_batched(start, n, &flat);
+    position_ = start + n;
+    const size_t V = static_cast<size_t>(info_.vocab);
+    out.reserve(n);
+    for (size_t i = 0; i < n; ++i)
+        out.emplace_back(flat.begin() + static_cast<std::ptrdiff_t>(i * V),
+                         flat.begin() + static_cast<std::ptrdiff_t>((i + 1) * V));
     return out;
 }
 
@@ -519,7 +533,7 @@ std::vector<std::vector<float>> Model::evaluate_block(const std::vector<int>& to
 // as one scan over the chunk's positions (emprise_hip_delta_net_batch), and attention
 // runs over the chunk at once as FP32 GEMMs with a causal softmax
 // (emprise_hip_attention_batch). Op order is that of the unfused decode step.
-void Model::prefill_batched(size_t start, size_t count) {
+void Model::prefill_batched(size_t start, size_t count, std::vector<float>* logits) {
     constexpr size_t kPrefillChunk = 2048;
     HipBackend& b = *backend_;
     const emprise_model_info& d = info_;
@@ -591,6 +605,26 @@ void Model::prefill_batched(size_t start, size_t count) {
             b.dev_swiglu(pf_a_, pf_b_, static_cast<int>(T * F));
             b.dev_linear_batch(L.down, pf_a_, F, pf_c_, H, T);
             b.dev_add(pf_x_, pf_c_, static_cast<int>(T * H));
+        }
+        if (logits) {
+            // the output norm and head over the chunk's rows, kHeadRows at a time
+            constexpr int kHeadRows = 64;
+            const uint64_t V = static_cast<uint64_t>(d.vocab);
+            if (!pf_logits_) pf_logits_ = b.dev_alloc(kHeadRows * V * 4);
+            b.dev_rmsnorm_rows(pf_x_, output_norm_, pf_xn_, static_cast<int>(H), T, d.eps);
+            for (int r0 = 0; r0 < T; r0 += kHeadRows) {
+                const int n = std::min(kHeadRows, T - r0);
+                b.dev_linear_batch(output_, pf_xn_ + static_cast<uint64_t>(r0) * H * 4, H, pf_logits_, V, n);
+                const size_t at = logits->size();
+                logits->resize(at + static_cast<size_t>(n) * V);
+                b.dev_download(logits->data() + at, pf_logits_, static_cast<size_t>(n) * V * 4);
+            }
+            if (p0 + T == count) {
+                // the last position's residual, as a decode step leaves it (last_hidden)
+                b.dev_fill(x_[0], 0.f, H);
+                b.dev_add(x_[0], pf_x_ + static_cast<uint64_t>(T - 1) * H * 4, static_cast<int>(H));
+                last_x_ = 0;
+            }
         }
     }
 }

@@ -74,8 +74,9 @@ private:
     emprise_weight upload(const std::string& name, uint64_t cols, uint64_t rows);
     emprise_weight upload_vector(const std::string& name, uint64_t n);
     void enqueue_step(bool logits);  // one position, reading token/position from dev_state_
-    // positions [start, start + count) of the tokens at dev_prompt_ in batches
-    void prefill_batched(size_t start, size_t count);
+    // positions [start, start + count) of the tokens at dev_prompt_ in batches; with
+    // logits, every position's output-head row is appended to it (count x vocab)
+    void prefill_batched(size_t start, size_t count, std::vector<float>* logits = nullptr);
     void set_state(int position, int token, int prompt_len);
     // evaluates seq from position 0 (no logits), leaving position_ = seq.size()
     void replay(const std::vector<int>& seq);
@@ -96,7 +97,7 @@ private:
     emprise_graph graph_full_ = 0, graph_prefill_ = 0;
     // batched prefill buffers, sized for pf_rows_ tokens on first use
     size_t pf_rows_ = 0;
-    emprise_dev pf_x_ = 0, pf_xn_ = 0, pf_a_ = 0, pf_b_ = 0, pf_c_ = 0;
+    emprise_dev pf_x_ = 0, pf_xn_ = 0, pf_a_ = 0, pf_b_ = 0, pf_c_ = 0, pf_logits_ = 0;
     bool have_graph_full_ = false, have_graph_prefill_ = false;
     // the MTP block: its weights (an attention layer + FFN in `layer`), its own K/V cache
     // of `length` rows, and buffers: cat = [enorm(e) | hnorm(h)], cur = eh_proj(cat), x =

@@ -65,12 +65,16 @@ def test_linear_lm_head(backend, wtype):
 
 
 @pytest.mark.parametrize("wtype,K,rows,cols", [(Q6_K, 3, 64, 512), (Q6_K, 37, 300, 512), (Q4_K, 130, 257, 4096),
-                                               (F32, 9, 33, 256), (Q6_K, 64, 512, 12288), (F16, 20, 40, 1536)])
+                                               (F32, 9, 33, 256), (Q6_K, 64, 512, 12288), (F16, 20, 40, 1536),
+                                               (Q6_K, 2, 4096, 4096), (Q4_K, 4, 1000, 4096), (Q6_K, 5, 333, 8192),
+                                               (Q6_K, 7, 257, 12288), (Q4_K, 4, 4096, 12288), (Q6_K, 3, 151936, 4096)])
 def test_linear_batch(backend, wtype, K, rows, cols):
     """Backend::linear_batch (backend.hpp:20-24): Y[k] = W X[k]. From 8 tokens up it runs
-    as an FP32 GEMM on the matrix cores (exact dequantised weights, FP32 products);
-    every token must match the CPU matvec, and the single-token projection, to the
-    per-op bar (batched == sequential, reference tests/core.cpp:149-164)."""
+    as an FP32 GEMM on the matrix cores (exact dequantised weights, FP32 products); from 2
+    to 7 through a chunked Q6_K/Q4_K matrix as the small-batch matvec (up to 4 inputs per
+    launch, 3 at 12288 columns, the weights read once per launch); every token must match
+    the CPU matvec, and the single-token projection, to the per-op bar (batched ==
+    sequential, reference tests/core.cpp:149-164)."""
     rng = np.random.default_rng(K * 131 + rows + cols + wtype)
     raw = matrix(rng, wtype, rows, cols)
     X = rng.standard_normal((K, cols)).astype(np.float32)

@@ -110,17 +110,23 @@ def test_mtp_check_acceptance_counts(mtp_path):
         assert gpu_match.tolist() == ref_match.tolist()
 
 
-def test_evaluate_block_matches_oracle(mtp_path):
-    """Every position's logits of a 5-token block after a 12-token prefix."""
-    toks = synth_prompt(8, TINY["vocab"], 17)
+@pytest.mark.parametrize("n", [2, 5, 9])
+def test_evaluate_block_matches_oracle(mtp_path, n):
+    """Every position's logits of an n-token block after a 12-token prefix, the block in one
+    batched pass (small-batch matvec projections up to 7 positions, GEMM from 8), and the
+    state it leaves: the next decode step and last_hidden match the CPU's."""
+    toks = synth_prompt(8, TINY["vocab"], 12 + n + 1)
     ref = oracle.Model(mtp_path, context=256)
     with Model(mtp_path, context=256) as m:
         m.prefill(toks[:12], logits=False)
         for t in toks[:12]:
             ref.evaluate(t, logits=False)
-        got = m.evaluate_block(toks[12:])
-        for i, t in enumerate(toks[12:]):
+        got = m.evaluate_block(toks[12:12 + n])
+        assert got.shape == (n, TINY["vocab"])
+        for i, t in enumerate(toks[12:12 + n]):
             _check(got[i], ref.evaluate(t), f"block row {i}")
+        _check(m.last_hidden(), ref.last_hidden(), "last_hidden after the block")
+        _check(m.evaluate(toks[-1]), ref.evaluate(toks[-1]), "decode step after the block")
 
 
 def test_mtp_errors(tmp_path, mtp_path):
