@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import tempfile
 import time
@@ -222,8 +223,9 @@ def _graph_time_ms(be, fn, n=20, reps=5):
 
 def suite(args):
     """The benchmark spec's other configurations, one JSON line each on stdout:
-    C1 standalone matvecs (Q6_K, Q4_K, Q8 activations), C2 GDN step and attention at
-    the 9B shape, C4a batched prefill of 2048 tokens and C4b fast-q8 decode on the
+    C1 standalone matvecs (Q6_K, Q4_K, Q8 activations) and small batches of 2-4 inputs,
+    C2 GDN step and attention at the 9B shape, C4a batched prefill of 2048 tokens, a
+    draft-verification block against decode steps, and C4b fast-q8 decode on the
     Q4_K_M-mix model. Synthetic seeded inputs as in the tests (tests/synth.py)."""
     import numpy as np
     sys.path.insert(0, str(ROOT / "tests"))
@@ -252,6 +254,26 @@ def suite(args):
                 be.free(y)
                 be.weight_free(w)
         be.close()
+
+    # a7 small batches: K inputs through one matrix, the weights read once per launch
+    be = ea.HipBackend(0)
+    for wtype in (ea.Q6_K, ea.Q4_K):
+        for rows, cols in ((12288, 4096), (4096, 12288)):
+            rng = np.random.default_rng(rows + cols + 5)
+            raw = matrix(rng, wtype, rows, cols)
+            w = be.upload_weight(wtype, cols, rows, raw)
+            for K in (2, 3, 4):
+                X = be.to_device(rng.standard_normal((K, cols)).astype(np.float32))
+                Y = be.alloc(K * rows * 4)
+                ms = _graph_time_ms(be, lambda: be.linear_batch(w, X, Y, K))
+                emit({"config": "C1-batch", "op": "linear_batch (small-batch matvec)",
+                      "weights": "Q6_K" if wtype == ea.Q6_K else "Q4_K", "rows": rows, "cols": cols, "K": K,
+                      "us": round(ms * 1e3, 2), "us_per_input": round(ms * 1e3 / K, 2),
+                      "weight_GBps": round(len(raw) / (ms * 1e-3) / 1e9, 1)})
+                be.free(X)
+                be.free(Y)
+            be.weight_free(w)
+    be.close()
 
     be = ea.HipBackend(0)
     rng = np.random.default_rng(2)
@@ -300,6 +322,27 @@ def suite(args):
     emit({"config": "C4a", "op": "batched prefill, Q4_K_M mix, FP32 MFMA GEMM projections",
           "prompt_tokens": 2048, "seconds": round(arr[0], 4), "tok_per_s": round(2048 / arr[0], 1),
           "host_wall_s": round(wall, 3), "token_weight_bytes": per_tok})
+    model.close()
+    # MTP draft verification: a block of positions in one batched pass against one decode
+    # step per position (Model::evaluate_block, model.cpp:274-354)
+    model = ea.Model(path, context=4096)
+    model.prefill(prompt[:512], logits=False)
+    at = 512
+    for K in (2, 3, 4):
+        block, steps = [], []
+        for rep in range(6):  # the first repetition warms up and is not counted
+            t0 = time.perf_counter()
+            model.evaluate_block(prompt[at:at + K])
+            block.append(time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            for t in prompt[at + K:at + 2 * K]:
+                model.evaluate(t)
+            steps.append(time.perf_counter() - t0)
+            at += 2 * K
+        emit({"config": "verify", "op": "evaluate_block (one batched pass) vs K decode steps, Q4_K_M mix, "
+              "all logits to the host, median of 5", "K": K,
+              "block_ms": round(statistics.median(block[1:]) * 1e3, 3),
+              "steps_ms": round(statistics.median(steps[1:]) * 1e3, 3)})
     model.close()
     model = ea.Model(path, context=4096, fast_q8=True)
     model.generate(prompt[:8], 4)

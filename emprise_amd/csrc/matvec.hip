@@ -1065,12 +1065,98 @@ __global__ __launch_bounds__(256) void dequant_rows_1k_kernel(const uint8_t* w, 
 // linear_batch for 2 <= K <= kBatchMax rows of X (the reference's chunked prefill and
 // draft verification batch up to 4 positions, cuda.cpp:350-413, model.cpp:355-366). A
 // wave takes whole rows (rows v, v + waves, ...), loads each 4096-column chunk of its row
-// once -- the next chunk's loads in flight while the current one is computed -- and runs
-// the single-input arithmetic (scompute) on it once per staged input, so the K outputs of
-// a row are K single-input dot products over the same weight registers. The inputs sit
+// once -- the next chunk's loads in flight while the current one is computed -- decodes
+// it once and runs the single-input arithmetic (scompute's product chains) on it for every
+// staged input, so the K outputs of a row are K single-input dot products over the same
+// decoded weights. The inputs sit
 // in LDS side by side, each in the streaming kernels' lane layout with its unit sums;
 // one 16-wave workgroup per CU.
 constexpr int kBatchWaves = 16;
+
+// The codes of a chunk's unit as floats, converted once for all K inputs (the
+// conversions are exact, so every product and sum below is scompute's for that input).
+__device__ __forceinline__ void codes4(uint32_t q, float* w) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = ubyte_f(q, i);
+}
+__device__ __forceinline__ float dot4f(const float* w, const float4& x, float acc) {
+    acc = fmaf(w[0], x.x, acc);
+    acc = fmaf(w[1], x.y, acc);
+    acc = fmaf(w[2], x.z, acc);
+    acc = fmaf(w[3], x.w, acc);
+    return acc;
+}
+
+// scompute<T, 1> of one weight item for K staged inputs (input k at xs + k * xstride,
+// its unit sums at usum + k * ustride): the weights are decoded once, then each input
+// runs scompute's product chains in scompute's order.
+template <int T, int K>
+__device__ __forceinline__ void scompute_k(const SChunk<T, 1>& ch, float* acc, const float* xs, size_t xstride,
+                                           const float* usum, size_t ustride, int c, int lane) {
+    if constexpr (T == kQ6K) {
+        const float dv = half_bits_to_float((uint16_t)ch.d[0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t d0 = lane_word(ch.q[0][0], j), d1 = lane_word(ch.q[0][1], j), d2 = lane_word(ch.q[0][2], j);
+            float wa[4], wb[4], wc[4], we[4];
+            codes4(opaque(d0 & 0x3F3F3F3Fu), wa);
+            codes4(opaque(d1 & 0x3F3F3F3Fu), wb);
+            codes4(opaque(d2 & 0x3F3F3F3Fu), wc);
+            codes4(opaque(((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u)), we);
+            const float scale = dv * (float)(int)(int8_t)(ch.sc[0] >> (8 * j));
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const float4* x4 = reinterpret_cast<const float4*>(xs + k * xstride) + (size_t)c * 1024 + lane;
+                const float4 off4 = reinterpret_cast<const float4*>(usum + k * ustride)[c * 64 + lane];
+                const float off = j == 0 ? off4.x : j == 1 ? off4.y : j == 2 ? off4.z : off4.w;
+                float4 xv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xv[i] = x4[(j * 4 + i) * 64];
+                float s0 = dot4f(wa, xv[0], off);
+                float s1 = dot4f(wb, xv[1], 0.f);
+                s0 = dot4f(wc, xv[2], s0);
+                s1 = dot4f(we, xv[3], s1);
+                acc[k] = fmaf(scale, s0 + s1, acc[k]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint4 d = ch.q[0][p];
+            float w[8][4];
+            codes4(opaque(d.x & 0x0F0F0F0Fu), w[0]);
+            codes4(opaque(d.y & 0x0F0F0F0Fu), w[1]);
+            codes4(opaque(d.z & 0x0F0F0F0Fu), w[2]);
+            codes4(opaque(d.w & 0x0F0F0F0Fu), w[3]);
+            codes4(opaque((d.x >> 4) & 0x0F0F0F0Fu), w[4]);
+            codes4(opaque((d.y >> 4) & 0x0F0F0F0Fu), w[5]);
+            codes4(opaque((d.z >> 4) & 0x0F0F0F0Fu), w[6]);
+            codes4(opaque((d.w >> 4) & 0x0F0F0F0Fu), w[7]);
+            const uint32_t b = (ch.s2[0] >> (8 * p)) & 0xff;
+            const int sc = b & 63;
+            const int mn = ((b >> 6) << 4) | ((ch.m4[0] >> (4 * p)) & 15);
+            const float dd = half_bits_to_float((uint16_t)(ch.dd[0] & 0xffff));
+            const float dm = half_bits_to_float((uint16_t)(ch.dd[0] >> 16));
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const float4* x4 = reinterpret_cast<const float4*>(xs + k * xstride) + (size_t)c * 1024 + lane;
+                const float2 xsum = reinterpret_cast<const float2*>(usum + k * ustride)[c * 64 + lane];
+                float4 xv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xv[i] = x4[(p * 8 + i) * 64];
+                float s0 = dot4f(w[0], xv[0], 0.f);
+                float s1 = dot4f(w[1], xv[1], 0.f);
+                s0 = dot4f(w[2], xv[2], s0);
+                s1 = dot4f(w[3], xv[3], s1);
+                s0 = dot4f(w[4], xv[4], s0);
+                s1 = dot4f(w[5], xv[5], s1);
+                s0 = dot4f(w[6], xv[6], s0);
+                s1 = dot4f(w[7], xv[7], s1);
+                acc[k] += (dd * (float)sc) * (s0 + s1) - (dm * (float)mn) * (p == 0 ? xsum.x : xsum.y);
+            }
+        }
+    }
+}
 
 template <int T, int K>
 __global__ __launch_bounds__(kBatchWaves * 64) void matvec_batch_kernel(MvBatchArgs a) {
@@ -1111,12 +1197,7 @@ __global__ __launch_bounds__(kBatchWaves * 64) void matvec_batch_kernel(MvBatchA
         sload<T, 1>(cur, rp, 0, lane);
         for (int c = 0; c < cpr; ++c) {
             if (c + 1 < cpr) sload<T, 1>(next, rp, c + 1, lane);
-#pragma unroll
-            for (int k = 0; k < K; ++k) {
-                float one[1] = {acc[k]};
-                scompute<T, 1>(cur, one, xs + (size_t)k * cols, usum + (size_t)k * units, c, lane);
-                acc[k] = one[0];
-            }
+            scompute_k<T, K>(cur, acc, xs, (size_t)cols, usum, (size_t)units, c, lane);
             cur = next;
         }
 #pragma unroll
