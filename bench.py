@@ -319,7 +319,7 @@ def suite(args):
     wall = time.perf_counter() - t0
     # weights applied per prompt token: every matrix but the output head, plus one embedding row
     per_tok = info.token_weight_bytes
-    emit({"config": "C4a", "op": "batched prefill, Q4_K_M mix, FP32 MFMA GEMM projections",
+    emit({"config": "C4a", "op": "batched prefill, Q4_K_M mix, projections on fp16 MFMA (exact fp16 pieces, FP32 sums)",
           "prompt_tokens": 2048, "seconds": round(arr[0], 4), "tok_per_s": round(2048 / arr[0], 1),
           "host_wall_s": round(wall, 3), "token_weight_bytes": per_tok})
     model.close()

@@ -834,10 +834,10 @@ emprise_status emprise_hip_linear_batch(emprise_hip* h, emprise_weight w, empris
 }
 
 // Y[k] = [W_0; W_1; ...] X[k]: the weights' rows side by side in Y, for K rows of X. From
-// kGemmMinBatch rows up the quantised rows are dequantised exactly into a scratch block
-// (weight by weight, each into its rows of the block) and the block runs as one GEMM, so
-// the weights of one input (q|k|v, the recurrent in-projections) share one launch and
-// its full tiles; below that, the streaming matvec per row of X.
+// kGemmMinBatch rows up the projections run as GEMMs on the matrix cores -- chunked
+// Q6_K/Q4_K weights on exact fp16 pieces, consecutive weights of one type (q|k|v, the
+// recurrent in-projections) sharing a launch and its full tiles; other weights
+// dequantised exactly to FP32 -- and below that as the streaming matvec per row of X.
 static emprise_status linear_batch_rows(emprise_hip* h, int nw, const Weight* const* ws, emprise_dev X, uint64_t ldx,
                                         emprise_dev Y, uint64_t ldy, int K) {
     const int cols = (int)ws[0]->cols;
@@ -885,30 +885,60 @@ static emprise_status linear_batch_rows(emprise_hip* h, int nw, const Weight* co
                                    cols, (int)ldy, h->stream);
         });
     }
-    // dequantise (or copy, for F32 rows) blocks of the stacked rows to FP32 (exact), then
-    // multiply
-    const uint64_t block = std::max<uint64_t>(128, kGemmScratchBytes / ((uint64_t)cols * 4) / 128 * 128);
-    const uint64_t nb = std::min<uint64_t>(block, rows);
-    void* wf;
-    TRY(h->get_scratch("gemm_w", nb * cols * sizeof(float), &wf));
-    for (uint64_t r0 = 0; r0 < rows; r0 += nb) {
-        const uint64_t n = std::min<uint64_t>(nb, rows - r0);
-        uint64_t first = 0;  // stacked index of weight i's row 0
-        for (int i = 0; i < nw; ++i) {
-            const Weight* wt = ws[i];
-            const uint64_t lo = std::max(first, r0), hi = std::min(first + wt->rows, r0 + n);
-            if (lo < hi) {
-                float* dst = static_cast<float*>(wf) + (lo - r0) * cols;
-                TRY(traced(h, "dequant_rows", (hi - lo) * (wt->bytes / wt->rows + (uint64_t)cols * 4), [&] {
-                    return launch_dequant_rows(wt->dev, wt->type, cols, lo - first, hi - lo, dst, h->stream);
-                }));
-            }
-            first += wt->rows;
-        }
-        TRY(traced(h, "gemm_f32", flops_per_row * n, [&] {
-            return launch_gemm_f32(A, static_cast<const float*>(wf), C + r0, K, (int)n, cols, (int)ldx, cols, (int)ldy,
-                                   h->stream);
+    // Chunked Q6_K / Q4_K weights run on the fp16 matrix cores (gemm_q.hip: exact fp16
+    // pieces of the weights and of the activations, FP32 sums), consecutive weights of one
+    // type in one launch; the others are dequantised (or copied, for F32 rows) exactly into
+    // FP32 blocks and multiplied in FP32.
+    auto on_q16 = [](const Weight* wt) { return (wt->type == kQ6K || wt->type == kQ4K) && chunked_cols(wt->cols); };
+    bool any_q = false, sums = false;
+    for (int i = 0; i < nw; ++i)
+        if (on_q16(ws[i])) any_q = true, sums = sums || ws[i]->type == kQ4K;
+    QGemmArgs qa{};
+    if (any_q) {
+        void* xs;
+        TRY(h->get_scratch("gemm_xs", gemm_q16_split_bytes(K, cols, sums), &xs));
+        TRY(traced(h, "split_f16", (uint64_t)K * cols * 8, [&] {
+            return launch_gemm_q16_split(A, K, cols, (int)ldx, xs, sums, &qa, h->stream);
         }));
+    }
+    const uint64_t block = std::max<uint64_t>(128, kGemmScratchBytes / ((uint64_t)cols * 4) / 128 * 128);
+    uint64_t first = 0;  // stacked index of weight i's row 0
+    for (int i = 0; i < nw;) {
+        if (on_q16(ws[i])) {
+            const uint32_t type = ws[i]->type;
+            int j = i, nr = 0;
+            qa.nseg = 0;
+            while (j < nw && on_q16(ws[j]) && ws[j]->type == type) {
+                qa.w[qa.nseg] = static_cast<const uint8_t*>(ws[j]->dev);
+                qa.row0[qa.nseg++] = nr;
+                nr += (int)ws[j]->rows;
+                ++j;
+            }
+            qa.row0[qa.nseg] = nr;
+            qa.N = nr;
+            qa.y = C + first;
+            qa.ldy = (int)ldy;
+            TRY(traced(h, "gemm_q16", flops_per_row * (uint64_t)nr, [&] { return launch_gemm_q16(type, qa, h->stream); }));
+            first += (uint64_t)nr;
+            i = j;
+            continue;
+        }
+        const Weight* wt = ws[i];
+        const uint64_t nb = std::min<uint64_t>(block, wt->rows);
+        void* wf;
+        TRY(h->get_scratch("gemm_w", nb * cols * sizeof(float), &wf));
+        for (uint64_t r0 = 0; r0 < wt->rows; r0 += nb) {
+            const uint64_t n = std::min<uint64_t>(nb, wt->rows - r0);
+            TRY(traced(h, "dequant_rows", n * (wt->bytes / wt->rows + (uint64_t)cols * 4), [&] {
+                return launch_dequant_rows(wt->dev, wt->type, cols, r0, n, static_cast<float*>(wf), h->stream);
+            }));
+            TRY(traced(h, "gemm_f32", flops_per_row * n, [&] {
+                return launch_gemm_f32(A, static_cast<const float*>(wf), C + first + r0, K, (int)n, cols, (int)ldx, cols,
+                                       (int)ldy, h->stream);
+            }));
+        }
+        first += wt->rows;
+        ++i;
     }
     return EMPRISE_OK;
 }

@@ -110,6 +110,26 @@ hipError_t launch_gemm_f32_heads(const float* A, const float* B, float* C, int M
                                  int ldc, int batch, int bdiv, size_t sA, size_t sB, size_t sC, bool causal_keys_n,
                                  bool causal_keys_k, int first, hipStream_t stream);
 
+// Batched projection on the fp16 matrix cores over chunked Q6_K / Q4_K weights
+// (gemm_q.hip): Y[m][n] = row n of the stacked weights . X[m], for up to kMaxSeg weights of
+// one type whose rows follow each other in Y. launch_gemm_q16_split fills the activation
+// fields from X (fp16 hi/lo pieces of 2^-e_m x, e_m per row, and with `sums` the pieces of
+// its 32-column sums) in `scratch` (gemm_q16_split_bytes); the caller fills the weights.
+struct QGemmArgs {
+    const uint16_t *xh, *xl, *sh, *sl;  // fp16 bits, [M][K] and [M][K/32]
+    const int* rexp;                    // [M]
+    int M, K;
+    const uint8_t* w[kMaxSeg];
+    int row0[kMaxSeg + 1];  // weight s holds rows [row0[s], row0[s+1])
+    int nseg, N;
+    float* y;
+    int ldy;
+};
+size_t gemm_q16_split_bytes(int M, int K, bool sums);
+hipError_t launch_gemm_q16_split(const float* X, int M, int K, int ldx, void* scratch, bool sums, QGemmArgs* a,
+                                 hipStream_t stream);
+hipError_t launch_gemm_q16(uint32_t type, const QGemmArgs& a, hipStream_t stream);
+
 // ---- Gated DeltaNet ----
 struct GdnArgs {
     int key_heads, value_heads, state_dim, conv_width;

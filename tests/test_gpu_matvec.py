@@ -67,14 +67,18 @@ def test_linear_lm_head(backend, wtype):
 @pytest.mark.parametrize("wtype,K,rows,cols", [(Q6_K, 3, 64, 512), (Q6_K, 37, 300, 512), (Q4_K, 130, 257, 4096),
                                                (F32, 9, 33, 256), (Q6_K, 64, 512, 12288), (F16, 20, 40, 1536),
                                                (Q6_K, 2, 4096, 4096), (Q4_K, 4, 1000, 4096), (Q6_K, 5, 333, 8192),
-                                               (Q6_K, 7, 257, 12288), (Q4_K, 4, 4096, 12288), (Q6_K, 3, 151936, 4096)])
+                                               (Q6_K, 7, 257, 12288), (Q4_K, 4, 4096, 12288), (Q6_K, 3, 151936, 4096),
+                                               (Q6_K, 8, 4096, 4096), (Q6_K, 200, 300, 4096), (Q4_K, 129, 1000, 8192),
+                                               (Q6_K, 40, 130, 12288), (Q4_K, 8, 128, 4096)])
 def test_linear_batch(backend, wtype, K, rows, cols):
     """Backend::linear_batch (backend.hpp:20-24): Y[k] = W X[k]. From 8 tokens up it runs
-    as an FP32 GEMM on the matrix cores (exact dequantised weights, FP32 products); from 2
-    to 7 through a chunked Q6_K/Q4_K matrix as the small-batch matvec (up to 4 inputs per
-    launch, 3 at 12288 columns, the weights read once per launch); every token must match
-    the CPU matvec, and the single-token projection, to the per-op bar (batched ==
-    sequential, reference tests/core.cpp:149-164)."""
+    on the matrix cores -- chunked Q6_K/Q4_K weights on exact fp16 pieces of weights and
+    activations with FP32 sums, other weights as an FP32 GEMM on exactly dequantised
+    weights; from 2 to 7 through a chunked Q6_K/Q4_K matrix as the small-batch matvec (up
+    to 4 inputs per launch, 3 at 12288 columns, the weights read once per launch); every
+    token must match the CPU matvec, and the single-token projection, to the per-op bar
+    (batched == sequential, reference tests/core.cpp:149-164). Token and row counts off
+    the 128 x 128 tiles included."""
     rng = np.random.default_rng(K * 131 + rows + cols + wtype)
     raw = matrix(rng, wtype, rows, cols)
     X = rng.standard_normal((K, cols)).astype(np.float32)
@@ -92,6 +96,36 @@ def test_linear_batch(backend, wtype, K, rows, cols):
             _close(Y[k], backend.download(y1, rows))
     for b in (xd, yd, x1, y1):
         backend.free(b)
+    backend.weight_free(w)
+
+
+@pytest.mark.parametrize("wtype", [Q6_K, Q4_K])
+def test_linear_batch_wide_range(backend, wtype):
+    """The fp16 GEMM scales each token row by a power of two before splitting it into fp16
+    pieces: rows of 1e6-sized, 1e-6-sized, mixed and all-zero activations (and one whose
+    values would overflow fp16 unscaled) all meet the per-op bar against the CPU matvec."""
+    rows, cols = 200, 4096
+    rng = np.random.default_rng(wtype + 5)
+    raw = matrix(rng, wtype, rows, cols)
+    X = rng.standard_normal((12, cols)).astype(np.float32)
+    X[0] *= 1e6
+    X[1] *= 1e-6
+    X[2, ::2] *= 1e5
+    X[3] = 0.0
+    X[4] *= 7e4  # beyond fp16's 65504 without the row scale
+    X[5, :100] = 0.0
+    w = backend.upload_weight(wtype, cols, rows, raw)
+    xd, yd = backend.to_device(X), backend.alloc(len(X) * rows * 4)
+    backend.linear_batch(w, xd, yd, len(X))
+    Y = backend.download(yd, (len(X), rows))
+    for k in range(len(X)):
+        ref = oracle.matvec(wtype, raw, X[k], rows)
+        if not np.any(ref):
+            assert np.all(Y[k] == 0.0), k
+        else:
+            _close(Y[k], ref)
+    backend.free(xd)
+    backend.free(yd)
     backend.weight_free(w)
 
 
