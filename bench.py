@@ -183,8 +183,8 @@ def attention_probe(kv_len: int, calls: int = 40):
 
 def gemm_probe(tokens: int, calls: int = 10):
     """Batched projection of `tokens` positions through a 12288 x 4096 Q6_K matrix (the
-    9B FFN gate shape) -- the prefill GEMM (dequantised FP32 rows on the matrix cores) --
-    `calls` times, for profilers; seeded synthetic weights and inputs."""
+    9B FFN gate shape) -- the prefill GEMM (fp16 pieces on the matrix cores) -- `calls`
+    times, for profilers; seeded synthetic weights and inputs."""
     import numpy as np
     sys.path.insert(0, str(ROOT / "tests"))
     from synth import matrix
@@ -200,6 +200,19 @@ def gemm_probe(tokens: int, calls: int = 10):
     be.sync()
     be.close()
     log(f"{calls} batched projections of {tokens} tokens through {rows} x {cols} Q6_K")
+
+
+def prefill_probe(tokens: int):
+    """Two batched prefills of a `tokens`-token seeded prompt through the 9B Q4_K_M mix
+    (C4a's workload), for profilers."""
+    import emprise_amd as ea
+    path = model_file("9b_q4km", seed=0)
+    model = ea.Model(path, context=4096)
+    prompt = ea.synth_prompt(1, model.info.vocab, tokens + 1)
+    for _ in range(2):
+        _, arr = model.generate(prompt, 1)
+        log(f"prefill of {tokens} tokens: {arr[0]:.4f} s")
+    model.close()
 
 
 def _graph_time_ms(be, fn, n=20, reps=5):
@@ -376,6 +389,8 @@ def main():
                     help="only run 40 eager 9B-shape attention calls over KV_LEN positions (for profilers) and exit")
     ap.add_argument("--gemm-probe", type=int, metavar="TOKENS",
                     help="only run 10 batched 12288x4096 Q6_K projections of TOKENS positions (for profilers) and exit")
+    ap.add_argument("--prefill-probe", type=int, metavar="TOKENS",
+                    help="only run two batched prefills of TOKENS positions on the 9B Q4_K_M mix (for profilers)")
     ap.add_argument("--suite", action="store_true",
                     help="only run the other benchmark configurations (C1, C2, C4), one JSON line each")
     args = ap.parse_args()
@@ -388,6 +403,9 @@ def main():
         return
     if args.gemm_probe:
         gemm_probe(args.gemm_probe)
+        return
+    if args.prefill_probe:
+        prefill_probe(args.prefill_probe)
         return
     if args.attention_probe:
         attention_probe(args.attention_probe)

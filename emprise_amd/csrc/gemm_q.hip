@@ -21,13 +21,14 @@
 // result is scaled back by 2^e_m. Only the rounding of the FP32 sums differs from the CPU
 // path's sequential row sum.
 //
-// Tiling: a workgroup of 8 waves computes 128 tokens x 128 rows; wave w owns tokens
-// 32*(w%4) .. +31 and rows 64*(w/4) .. +63 as two 32x32 v_mfma_f32_32x32x16_f16 tiles.
-// The K loop takes 64 columns per step (a quarter of a block; in the chunked layout the
-// 64 columns of matvec lane s of a chunk): the next step's split activations and raw
-// weight words are loaded into registers while the matrix cores work on the current
-// step from LDS, and each thread decodes its row's 16 (Q6_K) or 16-of-32 (Q4_K) codes of
-// the step into fp16 while storing them.
+// Tiling: a workgroup of 8 waves computes 128 tokens x 128 rows. Waves 0..3 multiply:
+// wave c owns tokens 64*(c%2) .. +63 and rows 64*(c/2) .. +63 as 2 x 2 tiles of
+// v_mfma_f32_32x32x16_f16. Waves 4..7 stage: the K loop takes 64 columns per step (a
+// quarter of a block; in the chunked layout the 64 columns of matvec lane s of a chunk)
+// from two LDS buffers, and while the multiplying waves run step s from one, the staging
+// waves decode step s+1's codes into fp16, store them with the activation pieces into the
+// other and issue the global loads of step s+3 (two register sets in turn); one barrier
+// per step.
 //
 // MFMA 32x32x16 f16 operand layout (lane l): A[i][k] with i = l % 32, k = 8*(l/32) + 0..7;
 // B[k][j] with j = l % 32, the same k; D[i][j] in accumulator r with j = l % 32 and
@@ -62,12 +63,23 @@ __device__ __forceinline__ uint32_t gld1(const void* p) { return *(const QGLOBAL
 
 // ---- activations: fp16 hi/lo pieces of 2^-e_m * x, and (for Q4_K) of its 32-column sums ----
 
-__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ X, int K, int ldx,
+// The pieces are stored tile by tile, in the order the GEMM reads them: tile (m/128,
+// k/64) is 128 x 64 halves, row-major, so a step's activation tile is one contiguous
+// 16 KiB run per piece. Rows from M up to the next multiple of 128 are zero.
+__device__ __forceinline__ size_t tiled(int m, int k, int K) {
+    return ((size_t)(m >> 7) * (K >> 6) + (k >> 6)) * (128 * 64) + (m & 127) * 64 + (k & 63);
+}
+
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ X, int M, int K, int ldx,
                                                          _Float16* __restrict__ xh, _Float16* __restrict__ xl,
                                                          int* __restrict__ rexp, _Float16* __restrict__ sh,
                                                          _Float16* __restrict__ sl) {
     __shared__ float red[8];
     const int m = blockIdx.x;
+    if (m >= M) {  // padding rows of the last tile
+        for (int i = threadIdx.x; i < K; i += blockDim.x) xh[tiled(m, i, K)] = xl[tiled(m, i, K)] = (_Float16)0.f;
+        return;
+    }
     const float* x = X + (size_t)m * ldx;
     float mx = 0.f;
     for (int i = threadIdx.x; i < K; i += blockDim.x) mx = fmaxf(mx, fabsf(x[i]));
@@ -82,13 +94,11 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
         e -= 1;                // mx * 2^-e in [1, 2)
     }
     if (threadIdx.x == 0) rexp[m] = e;
-    _Float16* ho = xh + (size_t)m * K;
-    _Float16* lo = xl + (size_t)m * K;
     for (int i = threadIdx.x; i < K; i += blockDim.x) {
         const float v = ldexpf(x[i], -e);
         const _Float16 h = (_Float16)v;
-        ho[i] = h;
-        lo[i] = (_Float16)(v - (float)h);
+        xh[tiled(m, i, K)] = h;
+        xl[tiled(m, i, K)] = (_Float16)(v - (float)h);
     }
     if (sh) {
         const int units = K / 32;
@@ -106,9 +116,9 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
 
 template <int T> struct QRaw;
 template <> struct QRaw<kQ6K> {
-    uint32_t d0, d1, d2;  // word j of the three code planes
-    int32_t sc;           // the unit's int8 scale
-    uint32_t d;           // fp16 block scale (read at a block's first step)
+    uint2 d0, d1, d2;  // words j0, j0+1 of the three code planes (units j0, j0+1)
+    uint32_t sc;       // the two units' int8 scales (low byte: unit j0)
+    uint32_t d;        // fp16 block scale (used at a block's first step)
 };
 template <> struct QRaw<kQ4K> {
     uint4 q;      // the unit's 32 nibbles
@@ -117,212 +127,299 @@ template <> struct QRaw<kQ4K> {
     uint32_t dd;  // fp16 d | fp16 dmin << 16
 };
 
+// Q6_K unit -> fp16 pieces: codes 0..3 in the low 6 bits of word d0, 4..7 of d1, 8..11 of
+// d2, 12..15 gathered from their top two bits; v = sc * (q - 32), exact in FP32, vh = v
+// with its significand cut to fp16's 11 bits, vl = v - vh.
+__device__ __forceinline__ void q6_unit_f16(uint32_t d0, uint32_t d1, uint32_t d2, int sc, _Float16* dh,
+                                            _Float16* dl) {
+    const uint32_t w[4] = {d0 & 0x3F3F3F3Fu, d1 & 0x3F3F3F3Fu, d2 & 0x3F3F3F3Fu,
+                           ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u)};
+    const float scf = (float)sc, zp = -32.f * scf;
+    uint32_t hi[8], lo[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float v0 = fmaf(ubyte_f(w[k], 2 * h), scf, zp), v1 = fmaf(ubyte_f(w[k], 2 * h + 1), scf, zp);
+            const float h0 = __uint_as_float(__float_as_uint(v0) & 0xFFFFE000u);
+            const float h1 = __uint_as_float(__float_as_uint(v1) & 0xFFFFE000u);
+            hi[2 * k + h] = pack_rtz(h0, h1);
+            lo[2 * k + h] = pack_rtz(v0 - h0, v1 - h1);
+        }
+    }
+    *reinterpret_cast<uint4*>(dh) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    *reinterpret_cast<uint4*>(dh + 8) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+    *reinterpret_cast<uint4*>(dl) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    *reinterpret_cast<uint4*>(dl + 8) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+}
+
+// Waves 0..3 multiply, waves 4..7 stage: with two LDS buffers and one barrier per step, the
+// staging waves decode and store step s+1 (and load step s+2) while the multiplying waves
+// run step s, so the weight decode, the LDS traffic and the matrix cores overlap.
 template <int T>
 __global__ __launch_bounds__(QThreads) void gemm_q16_kernel(QGemmArgs a) {
-    constexpr int NB = T == kQ6K ? 2 : 1;  // weight pieces
-    __shared__ __align__(16) _Float16 As[2][QM][QROW];
-    __shared__ __align__(16) _Float16 Bs[NB][QN][QROW];
-    __shared__ float ds[QN], dms[QN];
-    __shared__ __align__(16) _Float16 Ms[QN][8];  // Q4_K: -m of the block's 8 units
+    constexpr int NB = T == kQ6K ? 2 : 1;   // weight pieces
+    constexpr int NQ = T == kQ4K ? QN : 1;  // Q4_K-only arrays
+    // step s is read from buffer s%2 while step s+1 is stored into the other; the block
+    // scales and Q4_K mins by block parity
+    __shared__ __align__(16) _Float16 As[2][2][QM][QROW];
+    __shared__ __align__(16) _Float16 Bs[2][NB][QN][QROW];
+    __shared__ float ds[2][QN], dms[2][NQ];
+    __shared__ __align__(16) _Float16 Ms[2][NQ][8];  // Q4_K: -m of the block's 8 units
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.y * QM, n0 = blockIdx.x * QN;
-    const int wm = (wave & 3) * 32, wn = (wave >> 2) * 64;
     const int steps = a.K / QKS, cpr = a.K / kChunkCols;
+    const bool stager = wave >= 4;
 
-    // this thread's loads of a step: activations row ar (piece ap), columns ac .. ac+31;
-    // weights row bn = n0 + t/4, part bj = t%4 (Q6_K: unit bj; Q4_K: unit bj/2, half bj%2)
-    const int ap = t >> 8, ar = (t & 255) >> 1, ac = (t & 1) * 32;
-    const bool a_ok = m0 + ar < a.M;
-    const uint16_t* asrc = (ap ? a.xl : a.xh) + (size_t)(a_ok ? m0 + ar : 0) * a.K + ac;
-    const int bl = t >> 2, bj = t & 3, bn = n0 + bl;
-    const bool b_ok = bn < a.N;
-    // (rows past N read row 0 and are zeroed)
-    const uint8_t* brow;
-    {
-        const int r = b_ok ? bn : 0;
-        int s = 0;
-        while (s + 1 < a.nseg && r >= a.row0[s + 1]) ++s;
-        constexpr size_t kChunk = T == kQ6K ? 3360 : 2304;
-        brow = a.w[s] + (size_t)(r - a.row0[s]) * cpr * kChunk;
+    if (stager) {
+        // ---- staging waves: thread pt loads and stores four 16-byte pieces of each
+        // activation tile, and weight row pr, units 2*(pt%2), +1 (Q6_K) or unit pt%2 (Q4_K,
+        // both halves)
+        const int pt = threadIdx.x - 256, pr = pt >> 1, ph = pt & 1;
+        const size_t abase = (size_t)blockIdx.y * steps * (QM * QKS);  // the tile row's first step
+        const int bn = n0 + pr;
+        const bool b_ok = bn < a.N;
+        const uint8_t* brow;  // (rows past N read row 0 and are zeroed)
+        {
+            const int r = b_ok ? bn : 0;
+            int sg = 0;
+            while (sg + 1 < a.nseg && r >= a.row0[sg + 1]) ++sg;
+            constexpr size_t kChunk = T == kQ6K ? 3360 : 2304;
+            brow = a.w[sg] + (size_t)(r - a.row0[sg]) * cpr * kChunk;
+        }
+        // two register sets in turn (step k in set k%2): the loads of step k go out two
+        // steps before it is stored; every load is issued whatever the step (past the last
+        // step it re-reads the last one), so the waits for a set never cover the other's
+        struct Regs {
+            uint4 rh[4], rl[4];
+            QRaw<T> rb;
+        } R0, R1;
+        auto load_step = [&](int s, Regs& R) {
+            uint4* rh = R.rh;
+            uint4* rl = R.rl;
+            QRaw<T>& rb = R.rb;
+            s = min(s, steps - 1);
+            const int k0 = s * QKS;
+            // the step's 128 x 64 tile of each piece: 16 KiB in a row, 16 bytes per thread
+            // and load, a wave's load 1 KiB in a row
+            const size_t at = abase + (size_t)s * (QM * QKS);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                rh[i] = gld16(a.xh + at + 8 * (i * 256 + pt));
+                rl[i] = gld16(a.xl + at + 8 * (i * 256 + pt));
+            }
+            const int c = k0 / kChunkCols, ls = (k0 % kChunkCols) / QKS;  // chunk, matvec lane
+            if constexpr (T == kQ6K) {
+                const uint8_t* base = brow + (size_t)c * 3360 + 16 * ls + 8 * ph;
+                const uint32_t x0 = gld4(base), x1 = gld4(base + 4);
+                const uint32_t y0 = gld4(base + 1024), y1 = gld4(base + 1028);
+                const uint32_t z0 = gld4(base + 2048), z1 = gld4(base + 2052);
+                rb.d0 = make_uint2(x0, x1);
+                rb.d1 = make_uint2(y0, y1);
+                rb.d2 = make_uint2(z0, z1);
+                rb.sc = gld2(brow + (size_t)c * 3360 + 3072 + 4 * ls + 2 * ph);
+                rb.d = gld2(brow + (size_t)c * 3360 + 3328 + 2 * (ls >> 2));
+                if (!b_ok) rb = {make_uint2(0, 0), make_uint2(0, 0), make_uint2(0, 0), 0u, 0u};
+            } else {
+                const uint8_t* base = brow + (size_t)c * 2304;
+                rb.q = gld16(base + 1024 * ph + 16 * ls);
+                const uint8_t* sb = base + 2048 + 12 * (ls >> 2);
+                rb.s2 = gld2(sb + 2 * (ls & 3));
+                rb.m4 = gld1(sb + 8 + (ls & 3));
+                rb.dd = gld4(base + 2240 + 4 * (ls >> 2));
+                if (!b_ok) {
+                    rb.q = make_uint4(0, 0, 0, 0);
+                    rb.s2 = rb.m4 = rb.dd = 0u;
+                }
+            }
+        };
+        // registers -> LDS buffer `buf`: the activation pieces as they are, the weights
+        // decoded to fp16
+        auto store_step = [&](int s, int buf, const Regs& R) {
+            const uint4* rh = R.rh;
+            const uint4* rl = R.rl;
+            const QRaw<T>& rb = R.rb;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = i * 256 + pt;  // 16-byte piece e: row e/8, columns 8*(e%8) ..
+                *reinterpret_cast<uint4*>(&As[buf][0][e >> 3][8 * (e & 7)]) = rh[i];
+                *reinterpret_cast<uint4*>(&As[buf][1][e >> 3][8 * (e & 7)]) = rl[i];
+            }
+            const bool block_start = (s & 3) == 0;
+            const int bp = (s >> 2) & 1;
+            if constexpr (T == kQ6K) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int j = 2 * ph + u;
+                    q6_unit_f16(u ? rb.d0.y : rb.d0.x, u ? rb.d1.y : rb.d1.x, u ? rb.d2.y : rb.d2.x,
+                                (int)(int8_t)(rb.sc >> (8 * u)), &Bs[buf][0][pr][16 * j], &Bs[buf][NB - 1][pr][16 * j]);
+                }
+                if (block_start && ph == 0) ds[bp][pr] = half_bits_to_float((uint16_t)rb.d);
+            } else {
+                // unit p = ph of the step: codes 0..15 in the low nibbles of its four words,
+                // 16..31 in the high ones
+                const uint32_t b = (rb.s2 >> (8 * ph)) & 0xffu;
+                const float scf = (float)(b & 63u);
+                const uint32_t wv[4] = {rb.q.x, rb.q.y, rb.q.z, rb.q.w};
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    uint32_t pk[8];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t nib = (wv[k] >> (4 * hf)) & 0x0F0F0F0Fu;
+                        pk[2 * k] = pack_rtz(ubyte_f(nib, 0) * scf, ubyte_f(nib, 1) * scf);
+                        pk[2 * k + 1] = pack_rtz(ubyte_f(nib, 2) * scf, ubyte_f(nib, 3) * scf);
+                    }
+                    _Float16* dh = &Bs[buf][0][pr][32 * ph + 16 * hf];
+                    *reinterpret_cast<uint4*>(dh) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                    *reinterpret_cast<uint4*>(dh + 8) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+                }
+                const uint32_t mn = ((b >> 6) << 4) | ((rb.m4 >> (4 * ph)) & 15u);
+                Ms[bp][pr % NQ][2 * (s & 3) + ph] = (_Float16)(-(float)mn);
+                if (block_start && ph == 0) {
+                    ds[bp][pr] = half_bits_to_float((uint16_t)(rb.dd & 0xffffu));
+                    dms[bp][pr % NQ] = half_bits_to_float((uint16_t)(rb.dd >> 16));
+                }
+            }
+        };
+        // (steps is even: K is a multiple of 4096)
+        load_step(0, R0);
+        load_step(1, R1);
+        store_step(0, 0, R0);
+        load_step(2, R0);
+        __syncthreads();
+        for (int s = 0; s < steps; s += 2) {
+            if (s + 1 < steps) store_step(s + 1, 1, R1);
+            load_step(s + 3, R1);
+            __syncthreads();
+            if (s + 2 < steps) store_step(s + 2, 0, R0);
+            load_step(s + 4, R0);
+            __syncthreads();
+        }
+        return;
     }
 
-    uint4 ra[4];
-    QRaw<T> rb;
-    auto load_step = [&](int s) {
-        const int k0 = s * QKS;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ra[i] = gld16(asrc + k0 + 8 * i);  // row clamped in range; zeroed past M
-            if (!a_ok) ra[i] = make_uint4(0, 0, 0, 0);
-        }
-        const int c = k0 / kChunkCols, ls = (k0 % kChunkCols) / QKS;  // chunk, matvec lane
-        if constexpr (T == kQ6K) {
-            const uint8_t* base = brow + (size_t)c * 3360;
-            rb.d0 = gld4(base + 16 * ls + 4 * bj);
-            rb.d1 = gld4(base + 1024 + 16 * ls + 4 * bj);
-            rb.d2 = gld4(base + 2048 + 16 * ls + 4 * bj);
-            rb.sc = (int8_t)gld1(base + 3072 + 4 * ls + bj);
-            rb.d = gld2(base + 3328 + 2 * (ls >> 2));
-            if (!b_ok) rb = {0u, 0u, 0u, 0, 0u};
-        } else {
-            const uint8_t* base = brow + (size_t)c * 2304;
-            const int p = bj >> 1;
-            rb.q = gld16(base + 1024 * p + 16 * ls);
-            const uint8_t* sb = base + 2048 + 12 * (ls >> 2);
-            rb.s2 = gld2(sb + 2 * (ls & 3));
-            rb.m4 = gld1(sb + 8 + (ls & 3));
-            rb.dd = gld4(base + 2240 + 4 * (ls >> 2));
-            if (!b_ok) {
-                rb.q = make_uint4(0, 0, 0, 0);
-                rb.s2 = rb.m4 = rb.dd = 0u;
-            }
-        }
-    };
-
-    // registers -> LDS: the activation pieces as they are, the weights decoded to fp16
-    auto store_step = [&](int s) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&As[ap][ar][ac + 8 * i]) = ra[i];
-        const bool block_start = (s & 3) == 0;
-        if constexpr (T == kQ6K) {
-            // unit bj: codes 0..3 in the low 6 bits of d0, 4..7 of d1, 8..11 of d2, and
-            // 12..15 gathered from their top two bits
-            const uint32_t w[4] = {rb.d0 & 0x3F3F3F3Fu, rb.d1 & 0x3F3F3F3Fu, rb.d2 & 0x3F3F3F3Fu,
-                                   ((rb.d0 >> 6) & 0x03030303u) | ((rb.d1 >> 4) & 0x0C0C0C0Cu) |
-                                       ((rb.d2 >> 2) & 0x30303030u)};
-            const float scf = (float)rb.sc, zp = -32.f * scf;
-            uint32_t hi[8], lo[8];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    // v = sc * (q - 32), exact in FP32; vh keeps its top 11 significant bits
-                    const float v0 = fmaf(ubyte_f(w[k], 2 * h), scf, zp), v1 = fmaf(ubyte_f(w[k], 2 * h + 1), scf, zp);
-                    const float h0 = __uint_as_float(__float_as_uint(v0) & 0xFFFFE000u);
-                    const float h1 = __uint_as_float(__float_as_uint(v1) & 0xFFFFE000u);
-                    hi[2 * k + h] = pack_rtz(h0, h1);
-                    lo[2 * k + h] = pack_rtz(v0 - h0, v1 - h1);
-                }
-            }
-            _Float16* dh = &Bs[0][bl][16 * bj];
-            _Float16* dl = &Bs[1][bl][16 * bj];
-            *reinterpret_cast<uint4*>(dh) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            *reinterpret_cast<uint4*>(dh + 8) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-            *reinterpret_cast<uint4*>(dl) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4*>(dl + 8) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-            if (block_start && bj == 0) ds[bl] = half_bits_to_float((uint16_t)rb.d);
-        } else {
-            // unit p = bj/2 of the step: codes 0..15 in the low nibbles of its four words,
-            // 16..31 in the high ones; this thread's half is bj%2
-            const int p = bj >> 1, hf = bj & 1;
-            const uint32_t b = (rb.s2 >> (8 * p)) & 0xffu;
-            const float scf = (float)(b & 63u);
-            const uint32_t wv[4] = {rb.q.x, rb.q.y, rb.q.z, rb.q.w};
-            uint32_t pk[8];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t nib = (wv[k] >> (4 * hf)) & 0x0F0F0F0Fu;
-                pk[2 * k] = pack_rtz(ubyte_f(nib, 0) * scf, ubyte_f(nib, 1) * scf);
-                pk[2 * k + 1] = pack_rtz(ubyte_f(nib, 2) * scf, ubyte_f(nib, 3) * scf);
-            }
-            _Float16* dh = &Bs[0][bl][32 * p + 16 * hf];
-            *reinterpret_cast<uint4*>(dh) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-            *reinterpret_cast<uint4*>(dh + 8) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-            if (hf == 0) {
-                const uint32_t mn = ((b >> 6) << 4) | ((rb.m4 >> (4 * p)) & 15u);
-                Ms[bl][2 * (s & 3) + p] = (_Float16)(-(float)mn);
-            }
-            if (block_start && bj == 0) {
-                ds[bl] = half_bits_to_float((uint16_t)(rb.dd & 0xffffu));
-                dms[bl] = half_bits_to_float((uint16_t)(rb.dd >> 16));
-            }
-        }
-    };
-
-    floatx16 acc[2], cb[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[nb][r] = cb[nb][r] = 0.f;
+    // ---- multiplying waves: wave c owns tokens 64*(c%2) .. +63 and rows 64*(c/2) .. +63
+    // as 2 x 2 tiles of 32 x 32
+    const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
     const int fr = lane & 31, fk = 8 * (lane >> 5);  // fragment row/column and k offset
-
-    load_step(0);
+    floatx16 acc[2][2], cb[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = cb[i][j][r] = 0.f;
+    half8 sh8[2] = {}, sl8[2] = {};  // Q4_K: the block's unit sums (lanes 0..31; 32..63 zero)
+    __syncthreads();
     for (int s = 0; s < steps; ++s) {
-        __syncthreads();  // the previous step's fragments and block scales have been read
-        store_step(s);
-        __syncthreads();
-        if (s + 1 < steps) load_step(s + 1);
+        const int buf = s & 1;
+        if (T == kQ4K && (s & 3) == 0) {
 #pragma unroll
-        for (int q = 0; q < QKS / 16; ++q) {
-            const half8 xh = *reinterpret_cast<const half8*>(&As[0][wm + fr][16 * q + fk]);
-            const half8 xl = *reinterpret_cast<const half8*>(&As[1][wm + fr][16 * q + fk]);
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                const int n = wn + 32 * nb + fr;
-                const half8 wh = *reinterpret_cast<const half8*>(&Bs[0][n][16 * q + fk]);
-                cb[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, wh, cb[nb], 0, 0, 0);
-                cb[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, wh, cb[nb], 0, 0, 0);
-                if constexpr (T == kQ6K) {
-                    const half8 wl = *reinterpret_cast<const half8*>(&Bs[NB - 1][n][16 * q + fk]);
-                    cb[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, wl, cb[nb], 0, 0, 0);
-                }
-            }
-        }
-        if ((s & 3) == 3) {
-            // block end: acc += d * (block products); Q4_K also adds -dmin * sum_u m_u * xsum_u
-            half8 sh8 = {}, sl8 = {};
-            if constexpr (T == kQ4K) {
-                // lanes 0..31: units 0..7 of the block for token m; lanes 32..63: zero (k 8..15)
-                const int m = m0 + wm + fr, blk = s >> 2;
+            for (int mb = 0; mb < 2; ++mb) {
+                const int m = m0 + wm + 32 * mb + fr, blk = s >> 2;
                 const bool ok = lane < 32 && m < a.M;
                 const size_t o = (size_t)(m < a.M ? m : 0) * (a.K / 32) + 8 * blk;
                 uint4 hv = gld16(a.sh + o), lv = gld16(a.sl + o);
                 if (!ok) hv = lv = make_uint4(0, 0, 0, 0);
-                sh8 = __builtin_bit_cast(half8, hv);
-                sl8 = __builtin_bit_cast(half8, lv);
+                sh8[mb] = __builtin_bit_cast(half8, hv);
+                sl8[mb] = __builtin_bit_cast(half8, lv);
             }
+        }
+        // fragments of 16-column slice q, read one slice ahead of its products; the products
+        // go out piece by piece over the four tiles, so consecutive MFMAs never depend on
+        // each other
+        half8 fx[2][2][2], fw[2][2][NB];  // [slice parity][tile][piece]
+        auto frags = [&](int q, int f) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                fx[f][i][0] = *reinterpret_cast<const half8*>(&As[buf][0][wm + 32 * i + fr][16 * q + fk]);
+                fx[f][i][1] = *reinterpret_cast<const half8*>(&As[buf][1][wm + 32 * i + fr][16 * q + fk]);
+#pragma unroll
+                for (int pc = 0; pc < NB; ++pc)
+                    fw[f][i][pc] = *reinterpret_cast<const half8*>(&Bs[buf][pc][wn + 32 * i + fr][16 * q + fk]);
+            }
+        };
+        frags(0, 0);
+#pragma unroll
+        for (int q = 0; q < QKS / 16; ++q) {
+            const int f = q & 1;
+            if (q + 1 < QKS / 16) frags(q + 1, f ^ 1);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+                    cb[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fx[f][mb][0], fw[f][nb][0], cb[mb][nb], 0, 0, 0);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+                    cb[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fx[f][mb][1], fw[f][nb][0], cb[mb][nb], 0, 0, 0);
+            if constexpr (T == kQ6K) {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb)
+                        cb[mb][nb] =
+                            __builtin_amdgcn_mfma_f32_32x32x16_f16(fx[f][mb][0], fw[f][nb][NB - 1], cb[mb][nb], 0, 0, 0);
+            }
+        }
+        if ((s & 3) == 3) {
+            // block end: acc += d * (block products); Q4_K also adds -dmin * sum_u m_u * xsum_u
+            const int bp = (s >> 2) & 1;
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
                 const int n = wn + 32 * nb + fr;
-                const float d = ds[n];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    acc[nb][r] = fmaf(d, cb[nb][r], acc[nb][r]);
-                    cb[nb][r] = 0.f;
-                }
+                const float d = ds[bp][n];
+                half8 mv = {};
+                float dm = 0.f;
                 if constexpr (T == kQ4K) {
-                    uint4 mr = *reinterpret_cast<const uint4*>(&Ms[n][0]);
+                    uint4 mr = *reinterpret_cast<const uint4*>(&Ms[bp][n % NQ][0]);
                     if (lane >= 32) mr = make_uint4(0, 0, 0, 0);
-                    const half8 mv = __builtin_bit_cast(half8, mr);
-                    floatx16 cm = {};
-                    cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh8, mv, cm, 0, 0, 0);
-                    cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl8, mv, cm, 0, 0, 0);
-                    const float dm = dms[n];
+                    mv = __builtin_bit_cast(half8, mr);
+                    dm = dms[bp][n % NQ];
+                }
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[nb][r] = fmaf(dm, cm[r], acc[nb][r]);
+                for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        acc[mb][nb][r] = fmaf(d, cb[mb][nb][r], acc[mb][nb][r]);
+                        cb[mb][nb][r] = 0.f;
+                    }
+                    if constexpr (T == kQ4K) {
+                        floatx16 cm = {};
+                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh8[mb], mv, cm, 0, 0, 0);
+                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl8[mb], mv, cm, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[mb][nb][r] = fmaf(dm, cm[r], acc[mb][nb][r]);
+                    }
                 }
             }
         }
+        __syncthreads();
     }
 
     // Y[m][n] = 2^e_m * acc
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const int n = n0 + wn + 32 * nb + fr;
-        if (n >= a.N) continue;
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = m0 + wm + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-            if (m < a.M) a.y[(size_t)m * a.ldy + n] = ldexpf(acc[nb][r], a.rexp[m]);
+        for (int nb = 0; nb < 2; ++nb) {
+            const int n = n0 + wn + 32 * nb + fr;
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm + 32 * mb + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                if (m < a.M) a.y[(size_t)m * a.ldy + n] = ldexpf(acc[mb][nb][r], a.rexp[m]);
+            }
         }
-    }
 }
 
 }  // namespace
 
 size_t gemm_q16_split_bytes(int M, int K, bool sums) {
-    size_t b = (size_t)M * K * 2 * sizeof(_Float16) + (size_t)M * sizeof(int);
+    const size_t mp = (size_t)(M + QM - 1) / QM * QM;  // rows padded to whole tiles
+    size_t b = mp * K * 2 * sizeof(_Float16) + (size_t)M * sizeof(int);
     if (sums) b += (size_t)M * (K / 32) * 2 * sizeof(_Float16);
     return (b + 255) / 256 * 256;
 }
@@ -330,12 +427,13 @@ size_t gemm_q16_split_bytes(int M, int K, bool sums) {
 hipError_t launch_gemm_q16_split(const float* X, int M, int K, int ldx, void* scratch, bool sums, QGemmArgs* a,
                                  hipStream_t stream) {
     if (M < 1 || K < QKS || K % kChunkCols || ldx < K) return hipErrorInvalidValue;
+    const int mp = (M + QM - 1) / QM * QM;
     _Float16* xh = static_cast<_Float16*>(scratch);
-    _Float16* xl = xh + (size_t)M * K;
-    int* rexp = reinterpret_cast<int*>(xl + (size_t)M * K);
+    _Float16* xl = xh + (size_t)mp * K;
+    int* rexp = reinterpret_cast<int*>(xl + (size_t)mp * K);
     _Float16* sh = sums ? reinterpret_cast<_Float16*>(rexp + M) : nullptr;
     _Float16* sl = sums ? sh + (size_t)M * (K / 32) : nullptr;
-    launch_kernel(split_rows_kernel, dim3(M), dim3(256), 0, stream, X, K, ldx, xh, xl, rexp, sh, sl);
+    launch_kernel(split_rows_kernel, dim3(mp), dim3(256), 0, stream, X, M, K, ldx, xh, xl, rexp, sh, sl);
     a->xh = reinterpret_cast<const uint16_t*>(xh);
     a->xl = reinterpret_cast<const uint16_t*>(xl);
     a->rexp = rexp;

@@ -116,7 +116,7 @@ hipError_t launch_gemm_f32_heads(const float* A, const float* B, float* C, int M
 // fields from X (fp16 hi/lo pieces of 2^-e_m x, e_m per row, and with `sums` the pieces of
 // its 32-column sums) in `scratch` (gemm_q16_split_bytes); the caller fills the weights.
 struct QGemmArgs {
-    const uint16_t *xh, *xl, *sh, *sl;  // fp16 bits, [M][K] and [M][K/32]
+    const uint16_t *xh, *xl, *sh, *sl;  // fp16 bits: x in 128 x 64 tiles (gemm_q.hip), sums [M][K/32]
     const int* rexp;                    // [M]
     int M, K;
     const uint8_t* w[kMaxSeg];
