@@ -13,6 +13,8 @@
 // SiLU(gate) is applied before the single write of the head's output. Lane l of a wave
 // holds state columns l, l+64 (state_dim = 64*E), so every row access is one coalesced
 // 256-byte (E=1) or 512-byte (E=2) transfer.
+#include <utility>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -249,15 +251,47 @@ __global__ __launch_bounds__(256) void delta_conv_history_kernel(GdnBatchArgs a)
     }
 }
 
+// ---- prefill scan ------------------------------------------------------------------------
+//
+// The scan keeps each state row on the 16 lanes of a DPP row: lane j holds columns j,
+// j+16, ... (NE = state_dim/16 of them), so a wave carries four rows side by side and a
+// row's dot product is NE sequential FMAs per lane plus a four-step butterfly across its
+// 16 lanes. The per-position chain (decay, s.k, delta rule, s.q) is then about a third of
+// the instructions of a 64-lane row with two full-wave reductions per row.
+constexpr int kScanWaves = 4;   // waves per workgroup, four state rows each
+constexpr int kScanBlock = 64;  // positions per block: q/k staged in LDS, lane inputs in registers
+
+// Sum over the 16 lanes of each DPP row, left in all 16: swaps within quads, then the
+// half-row and row mirrors. Each step adds two equal partial sums (in either order, so
+// every lane gets the same bits).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xb1, 0xf>(0.f, v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4e, 0xf>(0.f, v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141, 0xf>(0.f, v);  // row_half_mirror
+    v += dpp_f<0x140, 0xf>(0.f, v);  // row_mirror
+    return v;
+}
+// lane U of each DPP row, in every lane of that row (row_newbcast)
+template <int U> __device__ __forceinline__ float row16_bcast(float v) { return dpp_f<0x150 + U, 0xf>(0.f, v); }
+// f(integral_constant<int, I>) for I = 0 .. N-1 in order (the DPP controls above are
+// immediates)
+template <class F, int... I> __device__ __forceinline__ void static_for_(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F> __device__ __forceinline__ void static_for(F&& f) {
+    static_for_(f, std::make_integer_sequence<int, N>{});
+}
+
 // The per-position inputs of the delta rule that every row of a head shares, computed
 // once per position instead of once per row: the L2-normalised q and k of each key head
 // (a wave per (position, key head), lane l keeping columns l, l+64 as gdn_kernel does, so
-// the sums and scales are gdn_kernel's bit for bit), stored lane-interleaved -- lane l's
-// q[l], q[l+64], k[l], k[l+64] are consecutive, one 16-byte load in the scan -- and the
-// decay and beta gate of each value head.
+// the sums and scales are gdn_kernel's bit for bit), and the decay and beta gate of each
+// value head. q|k are stored in the scan's lane order: the list of scan lane j is q at
+// columns j, j+16, ... then k at the same columns, cut into 16-byte chunks, and chunk c of
+// lane j sits at (c * 16 + j) * 4 -- a wave's read of one chunk is 256 consecutive bytes.
 template <int E>
 __global__ __launch_bounds__(256) void gdn_prep_batch_kernel(GdnBatchArgs a) {
-    constexpr int SD = 64 * E;
+    constexpr int SD = 64 * E, NE = SD / 16;
     const int lane = threadIdx.x & 63;
     const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);  // position * key_heads + key head
     const int key_dim = a.key_heads * SD, ch = 2 * key_dim + a.value_heads * SD;
@@ -276,11 +310,12 @@ __global__ __launch_bounds__(256) void gdn_prep_batch_kernel(GdnBatchArgs a) {
         qs = wave_sum(qs);
         ks = wave_sum(ks);
         const float qscale = 1.f / sqrtf(qs + a.eps) / sqrtf((float)SD), kscale = 1.f / sqrtf(ks + a.eps);
-        float* dst = a.qk + ((size_t)pair * 64 + lane) * 2 * E;
+        float* dst = a.qk + (size_t)pair * 2 * SD;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            dst[e] = qv[e] * qscale;
-            dst[E + e] = kv[e] * kscale;
+            const int col = lane + 64 * e, j = col & 15, iq = col >> 4, ik = NE + iq;
+            dst[((iq >> 2) * 16 + j) * 4 + (iq & 3)] = qv[e] * qscale;
+            dst[((ik >> 2) * 16 + j) * 4 + (ik & 3)] = kv[e] * kscale;
         }
     }
     const int i = blockIdx.x * 256 + threadIdx.x;  // position * value_heads + value head
@@ -291,138 +326,128 @@ __global__ __launch_bounds__(256) void gdn_prep_batch_kernel(GdnBatchArgs a) {
     }
 }
 
-template <int E> __device__ __forceinline__ void load_qk(const float* p, float (&q)[E], float (&k)[E]) {
-    if constexpr (E == 2) {
-        const float4 v = *reinterpret_cast<const float4*>(p);
-        q[0] = v.x, q[1] = v.y, k[0] = v.z, k[1] = v.w;
-    } else {
-        const float2 v = *reinterpret_cast<const float2*>(p);
-        q[0] = v.x, k[0] = v.y;
-    }
-}
-
-constexpr int kScanAhead = 8;  // positions whose q/k are in flight ahead of the one in use
-// workgroups per value head of the scan at state_dim 64 / 128: one row per wave (two
-// rows per wave measured the same, 15.9 ms per 2048-token 9B prefill: the chain of wave
-// reductions bounds it, not the loads)
-constexpr int kScanSplit1 = 8, kScanSplit2 = 16;
-
-// Rows [part*SD/SPLIT, (part+1)*SD/SPLIT) of value head h over all positions; RPW
-// consecutive rows per wave, their states in registers throughout. The chain per
-// position is the update itself -- two wave reductions per row, the rows' chains
-// interleaved -- with the inputs already in registers: q/k of the next kScanAhead
-// positions are in flight, and each row's v and the head's decay and beta gate of 64
-// positions arrive in one load each (lane u holds position t0 + u; the next 64 load while
-// these are used). The raw outputs S.q of 64 positions are collected the same way (lane
-// u) and written with one store per row.
-template <int E, int SPLIT>
-__global__ __launch_bounds__(kGdnWaves * 64) void gdn_scan_kernel(GdnBatchArgs a) {
-    constexpr int SD = 64 * E, RPW = SD / SPLIT / kGdnWaves, P = kScanAhead;
-    static_assert(RPW >= 1 && RPW <= 4, "rows per wave");
-    static_assert(64 % P == 0, "prefetch depth divides the 64-position block");
-    const int h = blockIdx.x / SPLIT, part = blockIdx.x - h * SPLIT, kh = h % a.key_heads;
+// The delta rule (backend.cpp:36-56) over all positions for 16 rows of value head h
+// (workgroup = h * SD/16 + part, wave w: rows part*16 + 4w .. +3, one per DPP row), the
+// states in registers throughout. Per block of 64 positions the workgroup stages the
+// block's q|k in LDS (loaded during the block before), and each lane holds its row's v,
+// and the head's decay and beta gate, of the block's positions (lane u: position t0 + u
+// for the gates; lane 16g + j: position t0 + 16q + j of row g for v); the raw outputs
+// S.q of 16 positions are collected in lanes and stored together. Row sums follow
+// row16_sum, so results differ from the 64-lane decode kernels (gdn_kernel,
+// gdn_rows_kernel) only in the order of FP32 additions.
+template <int E>
+__global__ __launch_bounds__(kScanWaves * 64) void gdn_scan_kernel(GdnBatchArgs a) {
+    constexpr int SD = 64 * E, NE = SD / 16, NC = NE / 2, PQK = 2 * SD;  // q|k floats per position
+    constexpr int RPB = kScanWaves * 4, F4 = kScanBlock * PQK / 4 / (kScanWaves * 64);
+    __shared__ __align__(16) float qks[2][kScanBlock][PQK];
+    const int parts = SD / RPB;
+    const int h = blockIdx.x / parts, part = blockIdx.x - h * parts, kh = h % a.key_heads;
     const int key_dim = a.key_heads * SD, ch = 2 * key_dim + a.value_heads * SD;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int d0 = part * (SD / SPLIT) + wave * RPW, last = a.count - 1;
-    float* S = a.state + (size_t)h * SD * SD + (size_t)d0 * SD;
-    float s[RPW][E];
+    const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row = part * RPB + wave * 4 + g, last = a.count - 1;
+    float* S = a.state + ((size_t)h * SD + row) * SD;
+    float s[NE];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r)
-#pragma unroll
-        for (int e = 0; e < E; ++e) s[r][e] = S[(size_t)r * SD + lane + 64 * e];
+    for (int i = 0; i < NE; ++i) s[i] = S[j + 16 * i];
 
-    const size_t qk_step = (size_t)a.key_heads * 64 * 2 * E;  // floats per position
-    const float* qk = a.qk + ((size_t)kh * 64 + lane) * 2 * E;
-    const float* v_col = a.conv_out + 2 * (size_t)key_dim + (size_t)h * SD + d0;
+    const float* qk = a.qk + (size_t)kh * PQK;
+    const size_t qk_step = (size_t)a.key_heads * PQK;  // floats per position
+    const float* v_col = a.conv_out + 2 * (size_t)key_dim + (size_t)h * SD + row;
     const size_t o_step = (size_t)a.value_heads * SD;
-    float* o_col = a.o + (size_t)h * SD + d0;
+    float* o_col = a.o + (size_t)h * SD + row;
 
-    float rq[P][E], rk[P][E];  // position t's q/k sit in slot t % P
-#pragma unroll
-    for (int u = 0; u < P; ++u) load_qk<E>(qk + (size_t)min(u, last) * qk_step, rq[u], rk[u]);
-    // lane u: the rows' v and the head's decay and beta gate of position t0 + u
-    struct Lanes {
-        float v[RPW], dec, b;
-    };
-    auto lane_inputs = [&](int t0, Lanes& l) {
-        const int t = min(t0 + lane, last);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) l.v[r] = v_col[(size_t)t * ch + r];
-        const float2 g = *reinterpret_cast<const float2*>(a.gates + 2 * ((size_t)t * a.value_heads + h));
-        l.dec = g.x, l.b = g.y;
-    };
-    // positions t0 .. t0+63 with their lane inputs in `cur`, while those of the next 64
-    // load into `nxt`
-    auto block = [&](int t0, const Lanes& cur, Lanes& nxt) {
-        lane_inputs(t0 + 64, nxt);
-        const int n = min(64, a.count - t0);
-        float ol[RPW];
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) ol[r] = 0.f;
-        for (int u0 = 0; u0 < n; u0 += P) {
-#pragma unroll
-            for (int j = 0; j < P; ++j) {
-                const int u = u0 + j, t = t0 + u;
-                if (u < n) {
-                    const float(&qv)[E] = rq[j];
-                    const float(&kv)[E] = rk[j];
-                    const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.dec), u));
-                    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.b), u));
-                    float mem[RPW], sum[RPW];
-#pragma unroll
-                    for (int r = 0; r < RPW; ++r) {
-                        mem[r] = 0.f;
-#pragma unroll
-                        for (int e = 0; e < E; ++e) {
-                            s[r][e] *= decay;
-                            mem[r] += s[r][e] * kv[e];
-                        }
-                    }
-#pragma unroll
-                    for (int r = 0; r < RPW; ++r) mem[r] = wave_sum(mem[r]);
-#pragma unroll
-                    for (int r = 0; r < RPW; ++r) {
-                        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.v[r]), u));
-                        const float delta = (v - mem[r]) * b;
-                        sum[r] = 0.f;
-#pragma unroll
-                        for (int e = 0; e < E; ++e) {
-                            s[r][e] += kv[e] * delta;
-                            sum[r] += s[r][e] * qv[e];
-                        }
-                    }
-#pragma unroll
-                    for (int r = 0; r < RPW; ++r) {
-                        sum[r] = wave_sum(sum[r]);
-                        ol[r] = lane == u ? sum[r] : ol[r];
-                    }
-                }
-                // refill the slot once its position is done, so the load lands in the same
-                // registers (a refill issued while the slot is still read needs a copy at
-                // the loop's back edge, and with it a wait for the load)
-                load_qk<E>(qk + (size_t)min(t + P, last) * qk_step, rq[j], rk[j]);
-            }
-        }
-        if (lane < n)
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) o_col[(size_t)(t0 + lane) * o_step + r] = ol[r];
-    };
-    // two register sets in turn, so no copy (and no wait for the next block's loads) sits
-    // between blocks
-    Lanes la, lb;
-    lane_inputs(0, la);
-    // Everything above has arrived before the loop starts, so the wait the compiler
-    // places before each slot's use is the steady state's (the loads of the following
-    // slots stay in flight), not one shaped by the order of these first loads.
-    __builtin_amdgcn_s_waitcnt(0);
-    for (int t0 = 0; t0 < a.count; t0 += 128) {
-        block(t0, la, lb);
-        if (t0 + 64 < a.count) block(t0 + 64, lb, la);
+    // the block's q|k: thread th moves float4 th + 256m, position (th + 256m) / (PQK/4)
+    // (plain loops in the kernel body: the array stays in registers)
+    typedef float f4v __attribute__((ext_vector_type(4)));  // (a native vector: HIP's float4 struct
+    f4v stage[F4];                                           // copies kept the array in scratch)
+#define EMPRISE_QK_LOAD(T0)                                                                                     \
+    _Pragma("unroll") for (int m = 0; m < F4; ++m) {                                                            \
+        const int f = threadIdx.x + kScanWaves * 64 * m, p = f / (PQK / 4), w = f - p * (PQK / 4);              \
+        stage[m] = *reinterpret_cast<const f4v*>(qk + (size_t)min((T0) + p, last) * qk_step + 4 * w);            \
     }
+#define EMPRISE_QK_STORE(BUF)                                                                                   \
+    _Pragma("unroll") for (int m = 0; m < F4; ++m) {                                                            \
+        const int f = threadIdx.x + kScanWaves * 64 * m, p = f / (PQK / 4), w = f - p * (PQK / 4);              \
+        *reinterpret_cast<f4v*>(&qks[(BUF)][p][4 * w]) = stage[m];                                              \
+    }
+    struct Lanes {
+        float v[kScanBlock / 16];
+        float2 dg;
+    };
+    auto lane_load = [&](int t0, Lanes& l) {
 #pragma unroll
-    for (int r = 0; r < RPW; ++r)
+        for (int q = 0; q < kScanBlock / 16; ++q) l.v[q] = v_col[(size_t)min(t0 + 16 * q + j, last) * ch];
+        // positions past the end leave the state as it is (decay 1, gate 0: s * 1 + k * 0,
+        // at most a zero's sign changes), so no position needs a branch
+        const float2 dg = *reinterpret_cast<const float2*>(a.gates + 2 * ((size_t)min(t0 + lane, last) * a.value_heads + h));
+        l.dg = t0 + lane <= last ? dg : make_float2(1.f, 0.f);
+    };
+
+    Lanes cur, nxt;
+    lane_load(0, cur);
+    EMPRISE_QK_LOAD(0)
+    EMPRISE_QK_STORE(0)
+    __syncthreads();
+    EMPRISE_QK_LOAD(kScanBlock)
+    for (int t0 = 0, buf = 0; t0 < a.count; t0 += kScanBlock, buf ^= 1) {
+        lane_load(t0 + kScanBlock, nxt);
+        // positions t0 + 16q .. +15
+        auto group = [&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            float ol = 0.f;
+            static_for<16>([&](auto uc) {
+                constexpr int uu = decltype(uc)::value;
+                const int u = 16 * q + uu;
+                {
+                    float qv[NE], kv[NE];
 #pragma unroll
-        for (int e = 0; e < E; ++e) S[(size_t)r * SD + lane + 64 * e] = s[r][e];
+                    for (int c = 0; c < NC / 2; ++c) {
+                        const float4 x = *reinterpret_cast<const float4*>(&qks[buf][u][(c * 16 + j) * 4]);
+                        const float4 y = *reinterpret_cast<const float4*>(&qks[buf][u][((c + NC / 2) * 16 + j) * 4]);
+                        qv[4 * c] = x.x, qv[4 * c + 1] = x.y, qv[4 * c + 2] = x.z, qv[4 * c + 3] = x.w;
+                        kv[4 * c] = y.x, kv[4 * c + 1] = y.y, kv[4 * c + 2] = y.z, kv[4 * c + 3] = y.w;
+                    }
+                    const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.dg.x), u));
+                    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.dg.y), u));
+                    const float vd = row16_bcast<uu>(cur.v[q]);
+                    float mem = 0.f;
+#pragma unroll
+                    for (int i = 0; i < NE; ++i) {
+                        s[i] *= decay;
+                        mem = fmaf(s[i], kv[i], mem);
+                    }
+                    mem = row16_sum(mem);
+                    const float delta = (vd - mem) * b;
+                    float sum = 0.f;
+#pragma unroll
+                    for (int i = 0; i < NE; ++i) {
+                        s[i] = fmaf(kv[i], delta, s[i]);
+                        sum = fmaf(s[i], qv[i], sum);
+                    }
+                    sum = row16_sum(sum);
+                    ol = j == uu ? sum : ol;
+                }
+            });
+            const int t = t0 + 16 * q + j;
+            if (t < a.count) o_col[(size_t)t * o_step] = ol;
+        };
+        static_assert(kScanBlock == 64, "four groups of 16 positions");
+        group(std::integral_constant<int, 0>{});
+        // the next block's q|k go into the buffer every wave finished reading before the
+        // last barrier, once the first 16 positions are done (their loads had that long)
+        EMPRISE_QK_STORE(buf ^ 1)
+        group(std::integral_constant<int, 1>{});
+        group(std::integral_constant<int, 2>{});
+        group(std::integral_constant<int, 3>{});
+        cur = nxt;
+        __syncthreads();
+        EMPRISE_QK_LOAD(t0 + 2 * kScanBlock)
+    }
+#undef EMPRISE_QK_LOAD
+#undef EMPRISE_QK_STORE
+#pragma unroll
+    for (int i = 0; i < NE; ++i) S[j + 16 * i] = s[i];
 }
 
 // Per-head RMSNorm with ssm_norm, then SiLU(gate) (backend.cpp:57-58), as gdn_kernel's
@@ -474,13 +499,13 @@ hipError_t launch_gdn_batch(const GdnBatchArgs& a, hipStream_t stream) {
 #undef EMPRISE_CONV_CASE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 block(kGdnWaves * 64);
     const int pgrid = std::max((a.count * a.key_heads + 3) / 4, (a.count * a.value_heads + 255) / 256);
     if (a.state_dim == 64) {
         launch_kernel(gdn_prep_batch_kernel<1>, dim3(pgrid), dim3(256), 0, stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
-        launch_kernel(gdn_scan_kernel<1, kScanSplit1>, dim3(a.value_heads * kScanSplit1), block, 0, stream, a);
+        launch_kernel(gdn_scan_kernel<1>, dim3(a.value_heads * 64 / (kScanWaves * 4)), dim3(kScanWaves * 64), 0,
+                      stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         launch_kernel(gdn_norm_gate_batch_kernel<1>, dim3(a.count * a.value_heads), dim3(64), 0, stream, a);
@@ -488,7 +513,8 @@ hipError_t launch_gdn_batch(const GdnBatchArgs& a, hipStream_t stream) {
         launch_kernel(gdn_prep_batch_kernel<2>, dim3(pgrid), dim3(256), 0, stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
-        launch_kernel(gdn_scan_kernel<2, kScanSplit2>, dim3(a.value_heads * kScanSplit2), block, 0, stream, a);
+        launch_kernel(gdn_scan_kernel<2>, dim3(a.value_heads * 128 / (kScanWaves * 4)), dim3(kScanWaves * 64), 0,
+                      stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         launch_kernel(gdn_norm_gate_batch_kernel<2>, dim3(a.count * a.value_heads), dim3(64), 0, stream, a);

@@ -162,7 +162,7 @@ struct GdnBatchArgs {
     float* conv_state;
     float* state;
     float* conv_out;
-    float* qk;     // count x key_heads x 64 lanes x 2*state_dim/64: normalised q then k per lane
+    float* qk;     // count x key_heads x 2*state_dim: normalised q|k in the scan's lane order
     float* gates;  // count x value_heads x {decay, sigmoid(beta)}
     float* o;
     float* out;
