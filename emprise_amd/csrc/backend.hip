@@ -1074,6 +1074,7 @@ emprise_status emprise_hip_delta_net(emprise_hip* h, const emprise_hip_delta_net
         return fail(EMPRISE_EINVAL, "Recurrent projection dimensions");
     if (!p->qkv || !p->gate || !p->alpha || !p->beta || !p->conv_state || !p->rec_state || !p->out)
         return fail(EMPRISE_EINVAL, "null buffer");
+    if (p->rec_state % 16) return fail(EMPRISE_EINVAL, "rec_state must be 16-byte aligned");
     void* conv_out;
     TRY(h->get_scratch("gdn_conv", (size_t)ch * sizeof(float), &conv_out));
     TRY(traced(h, "delta_conv", (uint64_t)ch * (p->conv_width * 8 + 8), [&] { return launch_delta_conv(reinterpret_cast<const float*>(p->qkv), reinterpret_cast<const float*>(conv->dev),
@@ -1112,6 +1113,7 @@ emprise_status emprise_hip_delta_net_noalloc(emprise_hip* h, const emprise_hip_d
         return fail(EMPRISE_EINVAL, "Recurrent projection dimensions");
     if (!p->qkv || !p->gate || !p->alpha || !p->beta || !p->conv_state || !p->rec_state || !p->out)
         return fail(EMPRISE_EINVAL, "null buffer");
+    if (p->rec_state % 16) return fail(EMPRISE_EINVAL, "rec_state must be 16-byte aligned");
     if (h->recording) return fail(EMPRISE_ESTATE, "delta_net_noalloc is not recorded into step programs");
     // the conv kernel writes all ch channels of the scratch before the state update reads
     // them, so nothing carried over from an earlier call is read
@@ -1149,6 +1151,7 @@ emprise_status emprise_hip_delta_net_batch(emprise_hip* h, const emprise_hip_del
         return fail(EMPRISE_EINVAL, "Recurrent projection dimensions");
     if (!p->qkv || !p->gate || !p->alpha || !p->beta || !p->conv_state || !p->rec_state || !p->out)
         return fail(EMPRISE_EINVAL, "null buffer");
+    if (p->rec_state % 16) return fail(EMPRISE_EINVAL, "rec_state must be 16-byte aligned");
     if (count < 1 || count > (1 << 19) || stride < (uint64_t)ch || out_stride < (uint64_t)vd)
         return fail(EMPRISE_EINVAL, "delta_net_batch: count %d, stride %llu, out_stride %llu", count,
                     (unsigned long long)stride, (unsigned long long)out_stride);
@@ -1203,6 +1206,7 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
         dt->rows * dt->cols != (uint64_t)p->value_heads || nw->rows * nw->cols != (uint64_t)p->state_dim)
         return fail(EMPRISE_EINVAL, "Recurrent projection dimensions");
     if (!p->conv_state || !p->rec_state) return fail(EMPRISE_EINVAL, "null state buffer");
+    if (p->rec_state % 16) return fail(EMPRISE_EINVAL, "rec_state must be 16-byte aligned");
     void* proj;
     const size_t proj_n = (size_t)ch + vd + 2 * (size_t)p->value_heads + vd;
     TRY(h->get_scratch("gdn_proj", proj_n * sizeof(float), &proj));

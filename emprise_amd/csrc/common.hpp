@@ -96,4 +96,80 @@ __device__ __forceinline__ float softplusf_(float x) { return fmaxf(x, 0.f) + lo
 // Byte j of a dword as float (v_cvt_f32_ubyte{j}).
 __device__ __forceinline__ float ubyte_f(uint32_t v, int j) { return (float)((v >> (8 * j)) & 0xffu); }
 
+// ---- Gated DeltaNet on 16-lane rows --------------------------------------------------
+//
+// Every GDN kernel (the decode kernels, the step program's phase, the prefill scan) keeps
+// a vector of SD = 16*NE columns -- a state row, q, k -- on the 16 lanes of a DPP row,
+// lane j holding columns NE*j .. NE*j + NE-1, so a wave carries four rows side by side.
+// A row sum is NE sequential FMAs per lane, then row16_sum; all the kernels use these
+// helpers, so they give the same bits.
+
+// Sum over the 16 lanes of each DPP row, left in all 16: swaps within quads, then the
+// half-row and row mirrors. Each step adds two equal partial sums (in either order, so
+// every lane gets the same bits).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xb1, 0xf>(0.f, v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4e, 0xf>(0.f, v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141, 0xf>(0.f, v);  // row_half_mirror
+    v += dpp_f<0x140, 0xf>(0.f, v);  // row_mirror
+    return v;
+}
+// lane U of each DPP row, in every lane of that row (row_newbcast)
+template <int U> __device__ __forceinline__ float row16_bcast(float v) { return dpp_f<0x150 + U, 0xf>(0.f, v); }
+
+// q/k L2 normalisation (backend.cpp:30-35): q / sqrt(sum q^2 + eps) / sqrt(SD) and
+// k / sqrt(sum k^2 + eps).
+template <int NE> __device__ __forceinline__ void gdn16_qk_norm(float (&q)[NE], float (&k)[NE], float eps) {
+    float qs = 0.f, ks = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        qs = fmaf(q[i], q[i], qs);
+        ks = fmaf(k[i], k[i], ks);
+    }
+    qs = row16_sum(qs);
+    ks = row16_sum(ks);
+    const float qscale = 1.f / sqrtf(qs + eps) / sqrtf((float)(16 * NE)), kscale = 1.f / sqrtf(ks + eps);
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        q[i] *= qscale;
+        k[i] *= kscale;
+    }
+}
+
+// The delta rule on one state row (backend.cpp:36-56) with normalised q/k, the head's
+// decay and beta gate b and the row's v: S *= decay; mem = S.k; S += k * (v - mem) * b;
+// returns S.q (in all 16 lanes of the row).
+template <int NE>
+__device__ __forceinline__ float gdn16_row(float (&s)[NE], const float (&q)[NE], const float (&k)[NE], float decay,
+                                           float b, float v) {
+    float mem = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        s[i] *= decay;
+        mem = fmaf(s[i], k[i], mem);
+    }
+    mem = row16_sum(mem);
+    const float delta = (v - mem) * b;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        s[i] = fmaf(k[i], delta, s[i]);
+        sum = fmaf(s[i], q[i], sum);
+    }
+    return row16_sum(sum);
+}
+
+// NE consecutive floats (NE a multiple of 4) as 16-byte accesses.
+template <int NE> __device__ __forceinline__ void ld16v(float (&d)[NE], const float* p) {
+#pragma unroll
+    for (int i = 0; i < NE; i += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p + i);
+        d[i] = v.x, d[i + 1] = v.y, d[i + 2] = v.z, d[i + 3] = v.w;
+    }
+}
+template <int NE> __device__ __forceinline__ void st16v(float* p, const float (&d)[NE]) {
+#pragma unroll
+    for (int i = 0; i < NE; i += 4) *reinterpret_cast<float4*>(p + i) = make_float4(d[i], d[i + 1], d[i + 2], d[i + 3]);
+}
+
 }  // namespace emprise

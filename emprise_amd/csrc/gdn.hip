@@ -6,13 +6,12 @@
 // outputs S.q; the per-head RMSNorm x gate then runs in the out-projection's input
 // staging, and the gate rows arrive already SiLU'd from the in-projection. gdn_kernel
 // (Backend::delta_net, and the other out-projection widths) does the whole head:
-// one workgroup per value head (8 waves). The head's q/k are L2-normalised inside the
-// workgroup (every wave redundantly; 2*state_dim values), the 64 KiB state of the head
-// is streamed once -- each wave loads all of its rows before any arithmetic so the
-// reads overlap -- updated in registers and written back, and the per-head RMSNorm x
-// SiLU(gate) is applied before the single write of the head's output. Lane l of a wave
-// holds state columns l, l+64 (state_dim = 64*E), so every row access is one coalesced
-// 256-byte (E=1) or 512-byte (E=2) transfer.
+// one workgroup per value head (8 waves), the per-head RMSNorm x SiLU(gate) applied
+// before the single write of the head's output. Both keep each state row on the 16 lanes
+// of a DPP row (common.hpp's gdn16 helpers: lane j holds state_dim/16 consecutive
+// columns, 16-byte accesses), four rows per wave side by side; every workgroup
+// L2-normalises the head's q/k itself (2*state_dim values), and each wave issues the
+// reads of all its state rows before any arithmetic so the reads overlap.
 #include <utility>
 
 #include "common.hpp"
@@ -42,67 +41,34 @@ __global__ void delta_conv_kernel(const float* qkv, const float* w, float* hist,
 
 template <int E>
 __global__ __launch_bounds__(kGdnWaves * 64) void gdn_kernel(GdnArgs a) {
-    constexpr int SD = 64 * E, RPW = SD / kGdnWaves;  // rows per wave
+    constexpr int SD = 64 * E, NE = SD / 16, P = SD / kGdnWaves / 4;  // passes of four rows per wave
     __shared__ float o_row[SD];
     const int h = blockIdx.x, kh = h % a.key_heads;  // tiled V-head order (backend.cpp:37)
     const int key_dim = a.key_heads * SD;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const float* q = a.qkv + (size_t)kh * SD;
-    const float* k = a.qkv + key_dim + (size_t)kh * SD;
+    const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const float* v = a.qkv + 2 * (size_t)key_dim + (size_t)h * SD;
     float* S = a.state + (size_t)h * SD * SD;
 
-    // issue the state reads of this wave's rows first; lane r also fetches v of row r
-    // (read back with readlane, so no load waits behind the state stores of the loop)
-    const float v_lane = lane < RPW ? v[wave * RPW + lane] : 0.f;
-    float s[RPW][E];
+    // the state reads of this wave's rows (wave * 4P + 4p + g) first, then v, q and k
+    float s[P][NE];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r)
+    for (int p = 0; p < P; ++p) ld16v<NE>(s[p], S + (size_t)(wave * 4 * P + 4 * p + g) * SD + NE * j);
+    float vd[P];
 #pragma unroll
-        for (int e = 0; e < E; ++e) s[r][e] = S[(size_t)(wave * RPW + r) * SD + lane + 64 * e];
-
-    // q/k L2 normalisation (backend.cpp:30-35): qscale = 1/sqrt(sum q^2 + eps)/sqrt(SD)
-    float qv[E], kv[E], qs = 0.f, ks = 0.f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        qv[e] = q[lane + 64 * e];
-        kv[e] = k[lane + 64 * e];
-        qs += qv[e] * qv[e];
-        ks += kv[e] * kv[e];
-    }
-    qs = wave_sum(qs);
-    ks = wave_sum(ks);
-    const float qscale = 1.f / sqrtf(qs + a.eps) / sqrtf((float)SD), kscale = 1.f / sqrtf(ks + a.eps);
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        qv[e] *= qscale;
-        kv[e] *= kscale;
-    }
+    for (int p = 0; p < P; ++p) vd[p] = v[wave * 4 * P + 4 * p + g];
+    float qv[NE], kv[NE];
+    ld16v<NE>(qv, a.qkv + (size_t)kh * SD + NE * j);
+    ld16v<NE>(kv, a.qkv + key_dim + (size_t)kh * SD + NE * j);
+    gdn16_qk_norm<NE>(qv, kv, a.eps);
     const float decay = expf(a.ssm_a[h] * softplusf_(a.alpha[h] + a.dt[h]));
     const float b = sigmoidf_(a.beta[h]);
-
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        const int d = wave * RPW + r;
-        float mem = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            s[r][e] *= decay;
-            mem += s[r][e] * kv[e];
-        }
-        mem = wave_sum(mem);
-        const float vd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_lane), r));
-        const float delta = (vd - mem) * b;
-        float sum = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            s[r][e] += kv[e] * delta;
-            sum += s[r][e] * qv[e];
-        }
-        sum = wave_sum(sum);
-#pragma unroll
-        for (int e = 0; e < E; ++e) S[(size_t)d * SD + lane + 64 * e] = s[r][e];
-        if (lane == 0) o_row[d] = sum;
+    for (int p = 0; p < P; ++p) {
+        const int d = wave * 4 * P + 4 * p + g;
+        const float sum = gdn16_row<NE>(s[p], qv, kv, decay, b, vd[p]);
+        st16v<NE>(S + (size_t)d * SD + NE * j, s[p]);
+        if (j == 0) o_row[d] = sum;
     }
     __syncthreads();
     // per-head RMSNorm with ssm_norm, then SiLU(gate) (backend.cpp:57-58)
@@ -114,77 +80,38 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_kernel(GdnArgs a) {
         const float scale = 1.f / sqrtf(ss / (float)SD + a.eps);
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            const int j = lane + 64 * e;
-            a.out[(size_t)h * SD + j] = o_row[j] * (scale * a.norm[j]) * siluf_(a.gate[(size_t)h * SD + j]);
+            const int c = lane + 64 * e;
+            a.out[(size_t)h * SD + c] = o_row[c] * (scale * a.norm[c]) * siluf_(a.gate[(size_t)h * SD + c]);
         }
     }
 }
 
 // The state update of rows [part*SD/SPLIT, (part+1)*SD/SPLIT) of value head h, with
-// workgroup blockIdx = h*SPLIT + part; each of the 8 waves owns RPW rows and writes their
-// raw outputs o[d] = S[d,:].q straight to global memory (no cross-wave step). q and k
-// are L2-normalised by every workgroup of the head (2*SD values).
+// workgroup blockIdx = h*SPLIT + part; each of the 8 waves owns four rows and writes
+// their raw outputs o[d] = S[d,:].q straight to global memory (no cross-wave step).
 template <int E, int SPLIT>
 __global__ __launch_bounds__(kGdnWaves * 64) void gdn_rows_kernel(GdnArgs a) {
-    constexpr int SD = 64 * E, RPW = SD / SPLIT / kGdnWaves;
-    static_assert(RPW >= 1 && RPW <= 64, "rows per wave");
+    constexpr int SD = 64 * E, NE = SD / 16;
+    static_assert(SD / SPLIT == 4 * kGdnWaves, "four rows per wave");
     const int h = blockIdx.x / SPLIT, part = blockIdx.x - h * SPLIT, kh = h % a.key_heads;
     const int key_dim = a.key_heads * SD;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int d0 = part * (SD / SPLIT) + wave * RPW;
-    const float* q = a.qkv + (size_t)kh * SD;
-    const float* k = a.qkv + key_dim + (size_t)kh * SD;
-    const float* v = a.qkv + 2 * (size_t)key_dim + (size_t)h * SD;
-    float* S = a.state + (size_t)h * SD * SD;
+    const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int d = part * (SD / SPLIT) + wave * 4 + g;  // this lane's row
+    float* Sd = a.state + ((size_t)h * SD + d) * SD + NE * j;
 
-    // all loads first: the wave's state rows, v of its rows (lane r holds row d0 + r),
-    // q and k
-    float s[RPW][E];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r)
-#pragma unroll
-        for (int e = 0; e < E; ++e) s[r][e] = S[(size_t)(d0 + r) * SD + lane + 64 * e];
-    const float v_lane = v[d0 + min(lane, RPW - 1)];
-    float qv[E], kv[E], qs = 0.f, ks = 0.f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        qv[e] = q[lane + 64 * e];
-        kv[e] = k[lane + 64 * e];
-        qs += qv[e] * qv[e];
-        ks += kv[e] * kv[e];
-    }
-    qs = wave_sum(qs);
-    ks = wave_sum(ks);
-    const float qscale = 1.f / sqrtf(qs + a.eps) / sqrtf((float)SD), kscale = 1.f / sqrtf(ks + a.eps);
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        qv[e] *= qscale;
-        kv[e] *= kscale;
-    }
+    // all loads first: the row's state, its v, q and k
+    float s[NE], qv[NE], kv[NE];
+    ld16v<NE>(s, Sd);
+    const float vd = a.qkv[2 * (size_t)key_dim + (size_t)h * SD + d];
+    ld16v<NE>(qv, a.qkv + (size_t)kh * SD + NE * j);
+    ld16v<NE>(kv, a.qkv + key_dim + (size_t)kh * SD + NE * j);
+    gdn16_qk_norm<NE>(qv, kv, a.eps);
     const float decay = expf(a.ssm_a[h] * softplusf_(a.alpha[h] + a.dt[h]));
     const float b = sigmoidf_(a.beta[h]);
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        float mem = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            s[r][e] *= decay;
-            mem += s[r][e] * kv[e];
-        }
-        mem = wave_sum(mem);
-        const float vd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_lane), r));
-        const float delta = (vd - mem) * b;
-        float sum = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            s[r][e] += kv[e] * delta;
-            sum += s[r][e] * qv[e];
-        }
-        sum = wave_sum(sum);
-#pragma unroll
-        for (int e = 0; e < E; ++e) S[(size_t)(d0 + r) * SD + lane + 64 * e] = s[r][e];
-        if (lane == 0) a.out[(size_t)h * SD + d0 + r] = sum;
-    }
+    const float sum = gdn16_row<NE>(s, qv, kv, decay, b, vd);
+    st16v<NE>(Sd, s);
+    if (j == 0) a.out[(size_t)h * SD + d] = sum;
 }
 
 // ---- batched form: `count` consecutive positions (the prompt prefill) -------------------
@@ -192,12 +119,12 @@ __global__ __launch_bounds__(kGdnWaves * 64) void gdn_rows_kernel(GdnArgs a) {
 // Position by position, the decode kernels above pay two launches and two dependent
 // memory round trips per position and layer. Over a prompt the three stages separate:
 // the conv1d is a scan per channel (one thread keeps a channel's history in registers
-// over all positions), the delta rule a scan per state row (one wave keeps its row in
-// registers over all positions) after a parallel pass that normalises q/k and forms the
-// decay and beta gate of every position, and the per-head RMSNorm x SiLU(gate) is
-// independent per position. Each step does the arithmetic of delta_conv_kernel and gdn_kernel in the
-// same order, so the outputs and the final states are those of `count` calls of the
-// per-position path.
+// over all positions), the delta rule a scan per state row (a DPP row keeps its state row
+// in registers over all positions) after a parallel pass that normalises q/k and forms
+// the decay and beta gate of every position, and the per-head RMSNorm x SiLU(gate) is
+// independent per position. Each step does the arithmetic of delta_conv_kernel and
+// gdn_kernel in the same order, so the outputs and the final states are those of `count`
+// calls of the per-position path.
 
 // conv1d + SiLU of every (position, channel). Output t reads only inputs t-CW+1 .. t
 // (the ones before the prompt from the history), so the positions are independent:
@@ -253,28 +180,15 @@ __global__ __launch_bounds__(256) void delta_conv_history_kernel(GdnBatchArgs a)
 
 // ---- prefill scan ------------------------------------------------------------------------
 //
-// The scan keeps each state row on the 16 lanes of a DPP row: lane j holds columns j,
-// j+16, ... (NE = state_dim/16 of them), so a wave carries four rows side by side and a
-// row's dot product is NE sequential FMAs per lane plus a four-step butterfly across its
-// 16 lanes. The per-position chain (decay, s.k, delta rule, s.q) is then about a third of
-// the instructions of a 64-lane row with two full-wave reductions per row.
+// One wave carries four state rows (one per DPP row, common.hpp's layout) through all
+// the positions; per position a lane runs NE multiplies, 3*NE FMAs and two 16-lane
+// butterflies, the chain a 64-lane row would run with two full-wave reductions per row
+// in about a third of the instructions.
 constexpr int kScanWaves = 4;   // waves per workgroup, four state rows each
 constexpr int kScanBlock = 64;  // positions per block: q/k staged in LDS, lane inputs in registers
 
-// Sum over the 16 lanes of each DPP row, left in all 16: swaps within quads, then the
-// half-row and row mirrors. Each step adds two equal partial sums (in either order, so
-// every lane gets the same bits).
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dpp_f<0xb1, 0xf>(0.f, v);   // quad_perm [1,0,3,2]
-    v += dpp_f<0x4e, 0xf>(0.f, v);   // quad_perm [2,3,0,1]
-    v += dpp_f<0x141, 0xf>(0.f, v);  // row_half_mirror
-    v += dpp_f<0x140, 0xf>(0.f, v);  // row_mirror
-    return v;
-}
-// lane U of each DPP row, in every lane of that row (row_newbcast)
-template <int U> __device__ __forceinline__ float row16_bcast(float v) { return dpp_f<0x150 + U, 0xf>(0.f, v); }
-// f(integral_constant<int, I>) for I = 0 .. N-1 in order (the DPP controls above are
-// immediates)
+// f(integral_constant<int, I>) for I = 0 .. N-1 in order (row16_bcast's lane is an
+// immediate)
 template <class F, int... I> __device__ __forceinline__ void static_for_(F&& f, std::integer_sequence<int, I...>) {
     (f(std::integral_constant<int, I>{}), ...);
 }
@@ -284,38 +198,31 @@ template <int N, class F> __device__ __forceinline__ void static_for(F&& f) {
 
 // The per-position inputs of the delta rule that every row of a head shares, computed
 // once per position instead of once per row: the L2-normalised q and k of each key head
-// (a wave per (position, key head), lane l keeping columns l, l+64 as gdn_kernel does, so
-// the sums and scales are gdn_kernel's bit for bit), and the decay and beta gate of each
-// value head. q|k are stored in the scan's lane order: the list of scan lane j is q at
-// columns j, j+16, ... then k at the same columns, cut into 16-byte chunks, and chunk c of
-// lane j sits at (c * 16 + j) * 4 -- a wave's read of one chunk is 256 consecutive bytes.
+// (gdn16_qk_norm on a DPP row per (position, key head), so the values are the decode
+// kernels' bit for bit), and the decay and beta gate of each value head. q|k are stored
+// in the scan's lane order: the list of lane j is its NE q columns then its NE k columns,
+// cut into 16-byte chunks, and chunk c of lane j sits at (c * 16 + j) * 4 -- a wave's read
+// of one chunk is 256 consecutive bytes.
 template <int E>
 __global__ __launch_bounds__(256) void gdn_prep_batch_kernel(GdnBatchArgs a) {
     constexpr int SD = 64 * E, NE = SD / 16;
-    const int lane = threadIdx.x & 63;
-    const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);  // position * key_heads + key head
+    const int j = threadIdx.x & 15;
+    const int pair = blockIdx.x * 16 + (threadIdx.x >> 4);  // position * key_heads + key head
     const int key_dim = a.key_heads * SD, ch = 2 * key_dim + a.value_heads * SD;
-    if (pair < a.count * a.key_heads) {
+    if (pair < a.count * a.key_heads) {  // (whole DPP rows, as the row sums need)
         const int t = pair / a.key_heads, kh = pair - t * a.key_heads;
         const float* row = a.conv_out + (size_t)t * ch;
-        // q/k L2 normalisation (backend.cpp:30-35), as gdn_kernel
-        float qv[E], kv[E], qs = 0.f, ks = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            qv[e] = row[(size_t)kh * SD + lane + 64 * e];
-            kv[e] = row[key_dim + (size_t)kh * SD + lane + 64 * e];
-            qs += qv[e] * qv[e];
-            ks += kv[e] * kv[e];
-        }
-        qs = wave_sum(qs);
-        ks = wave_sum(ks);
-        const float qscale = 1.f / sqrtf(qs + a.eps) / sqrtf((float)SD), kscale = 1.f / sqrtf(ks + a.eps);
+        float qv[NE], kv[NE];
+        ld16v<NE>(qv, row + (size_t)kh * SD + NE * j);
+        ld16v<NE>(kv, row + key_dim + (size_t)kh * SD + NE * j);
+        gdn16_qk_norm<NE>(qv, kv, a.eps);
         float* dst = a.qk + (size_t)pair * 2 * SD;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int col = lane + 64 * e, j = col & 15, iq = col >> 4, ik = NE + iq;
-            dst[((iq >> 2) * 16 + j) * 4 + (iq & 3)] = qv[e] * qscale;
-            dst[((ik >> 2) * 16 + j) * 4 + (ik & 3)] = kv[e] * kscale;
+        for (int c = 0; c < NE / 4; ++c) {
+            *reinterpret_cast<float4*>(dst + (c * 16 + j) * 4) =
+                make_float4(qv[4 * c], qv[4 * c + 1], qv[4 * c + 2], qv[4 * c + 3]);
+            *reinterpret_cast<float4*>(dst + ((NE / 4 + c) * 16 + j) * 4) =
+                make_float4(kv[4 * c], kv[4 * c + 1], kv[4 * c + 2], kv[4 * c + 3]);
         }
     }
     const int i = blockIdx.x * 256 + threadIdx.x;  // position * value_heads + value head
@@ -332,9 +239,8 @@ __global__ __launch_bounds__(256) void gdn_prep_batch_kernel(GdnBatchArgs a) {
 // block's q|k in LDS (loaded during the block before), and each lane holds its row's v,
 // and the head's decay and beta gate, of the block's positions (lane u: position t0 + u
 // for the gates; lane 16g + j: position t0 + 16q + j of row g for v); the raw outputs
-// S.q of 16 positions are collected in lanes and stored together. Row sums follow
-// row16_sum, so results differ from the 64-lane decode kernels (gdn_kernel,
-// gdn_rows_kernel) only in the order of FP32 additions.
+// S.q of 16 positions are collected in lanes and stored together. The update of a row is
+// gdn16_row, as in the decode kernels, with the prep kernel's q/k.
 template <int E>
 __global__ __launch_bounds__(kScanWaves * 64) void gdn_scan_kernel(GdnBatchArgs a) {
     constexpr int SD = 64 * E, NE = SD / 16, NC = NE / 2, PQK = 2 * SD;  // q|k floats per position
@@ -346,10 +252,9 @@ __global__ __launch_bounds__(kScanWaves * 64) void gdn_scan_kernel(GdnBatchArgs 
     const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row = part * RPB + wave * 4 + g, last = a.count - 1;
-    float* S = a.state + ((size_t)h * SD + row) * SD;
+    float* S = a.state + ((size_t)h * SD + row) * SD + NE * j;
     float s[NE];
-#pragma unroll
-    for (int i = 0; i < NE; ++i) s[i] = S[j + 16 * i];
+    ld16v<NE>(s, S);
 
     const float* qk = a.qk + (size_t)kh * PQK;
     const size_t qk_step = (size_t)a.key_heads * PQK;  // floats per position
@@ -411,21 +316,7 @@ __global__ __launch_bounds__(kScanWaves * 64) void gdn_scan_kernel(GdnBatchArgs 
                     const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.dg.x), u));
                     const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.dg.y), u));
                     const float vd = row16_bcast<uu>(cur.v[q]);
-                    float mem = 0.f;
-#pragma unroll
-                    for (int i = 0; i < NE; ++i) {
-                        s[i] *= decay;
-                        mem = fmaf(s[i], kv[i], mem);
-                    }
-                    mem = row16_sum(mem);
-                    const float delta = (vd - mem) * b;
-                    float sum = 0.f;
-#pragma unroll
-                    for (int i = 0; i < NE; ++i) {
-                        s[i] = fmaf(kv[i], delta, s[i]);
-                        sum = fmaf(s[i], qv[i], sum);
-                    }
-                    sum = row16_sum(sum);
+                    const float sum = gdn16_row<NE>(s, qv, kv, decay, b, vd);
                     ol = j == uu ? sum : ol;
                 }
             });
@@ -446,8 +337,7 @@ __global__ __launch_bounds__(kScanWaves * 64) void gdn_scan_kernel(GdnBatchArgs 
     }
 #undef EMPRISE_QK_LOAD
 #undef EMPRISE_QK_STORE
-#pragma unroll
-    for (int i = 0; i < NE; ++i) S[j + 16 * i] = s[i];
+    st16v<NE>(S, s);
 }
 
 // Per-head RMSNorm with ssm_norm, then SiLU(gate) (backend.cpp:57-58), as gdn_kernel's
@@ -499,7 +389,7 @@ hipError_t launch_gdn_batch(const GdnBatchArgs& a, hipStream_t stream) {
 #undef EMPRISE_CONV_CASE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int pgrid = std::max((a.count * a.key_heads + 3) / 4, (a.count * a.value_heads + 255) / 256);
+    const int pgrid = std::max((a.count * a.key_heads + 15) / 16, (a.count * a.value_heads + 255) / 256);
     if (a.state_dim == 64) {
         launch_kernel(gdn_prep_batch_kernel<1>, dim3(pgrid), dim3(256), 0, stream, a);
         e = hipGetLastError();

@@ -431,88 +431,60 @@ __device__ void step_matvec(const StepMatvec& m, uint32_t tag, uint32_t base, un
 // ---- Gated DeltaNet phase ------------------------------------------------------------------
 
 // gdn_rows_kernel's state update (gdn.hip) with tagged q/k/v/alpha/beta inputs: unit u =
-// value head u / SPLIT, rows part*(SD/SPLIT).. of it; RPW rows per wave, raw outputs S.q.
+// value head u / SPLIT, rows part*(SD/SPLIT).. of it, four rows per wave on the 16 lanes
+// of a DPP row each (common.hpp's gdn16 layout), raw outputs S.q.
 template <int E, int SPLIT>
 __device__ void step_gdn(const StepGdn& g, uint32_t tag, uint32_t base, Waiter& wt) {
-    constexpr int SD = 64 * E, RPW = SD / SPLIT / kStepWaves;
-    static_assert(RPW >= 1 && RPW <= 64, "rows per wave");
+    constexpr int SD = 64 * E, NE = SD / 16;
+    static_assert(SD / SPLIT == 4 * kStepWaves, "four rows per wave");
     const int units = g.value_heads * SPLIT;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wq = want_of(g.qkv, base), wa = want_of(g.alpha, base), wb = want_of(g.beta, base);
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
         const int h = u / SPLIT, part = u - h * SPLIT, kh = h % g.key_heads;  // tiled V heads (backend.cpp:37)
         const int key_dim = g.key_heads * SD;
-        const int d0 = part * (SD / SPLIT) + wave * RPW;
-        EMPRISE_GLOBAL float* S = gm(g.state) + (size_t)h * SD * SD;
-        float s[RPW][E];
+        const int d = part * (SD / SPLIT) + wave * 4 + (lane >> 4);  // this lane's row
+        EMPRISE_GLOBAL float* Sd = gm(g.state) + ((size_t)h * SD + d) * SD + NE * j;
+        float s[NE];
 #pragma unroll
-        for (int r = 0; r < RPW; ++r)
+        for (int i = 0; i < NE; ++i) s[i] = Sd[i];
+        const size_t vo = 2 * (size_t)key_dim + (size_t)h * SD + d;
+        uint64_t vr = ld_in(g.qkv, vo, wq);
+        uint64_t qr[NE], kr[NE];
 #pragma unroll
-            for (int e = 0; e < E; ++e) s[r][e] = S[(size_t)(d0 + r) * SD + lane + 64 * e];
-        uint64_t vr = ld_in(g.qkv, 2 * (size_t)key_dim + (size_t)h * SD + d0 + min(lane, RPW - 1), wq);
-        uint64_t qr[E], kr[E];
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            qr[e] = ld_in(g.qkv, (size_t)kh * SD + lane + 64 * e, wq);
-            kr[e] = ld_in(g.qkv, (size_t)key_dim + (size_t)kh * SD + lane + 64 * e, wq);
+        for (int i = 0; i < NE; ++i) {
+            qr[i] = ld_in(g.qkv, (size_t)kh * SD + NE * j + i, wq);
+            kr[i] = ld_in(g.qkv, (size_t)key_dim + (size_t)kh * SD + NE * j + i, wq);
         }
         uint64_t ar = ld_in(g.alpha, h, wa), br = ld_in(g.beta, h, wb);
         while (true) {
             bool ready = tag_ok(vr, wq) && tag_ok(ar, wa) && tag_ok(br, wb);
 #pragma unroll
-            for (int e = 0; e < E; ++e) ready = ready && tag_ok(qr[e], wq) && tag_ok(kr[e], wq);
+            for (int i = 0; i < NE; ++i) ready = ready && tag_ok(qr[i], wq) && tag_ok(kr[i], wq);
             if (ready || !wt.again()) break;
-            vr = repoll(vr, wq, g.qkv.p, 2 * (size_t)key_dim + (size_t)h * SD + d0 + min(lane, RPW - 1));
+            vr = repoll(vr, wq, g.qkv.p, vo);
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                qr[e] = repoll(qr[e], wq, g.qkv.p, (size_t)kh * SD + lane + 64 * e);
-                kr[e] = repoll(kr[e], wq, g.qkv.p, (size_t)key_dim + (size_t)kh * SD + lane + 64 * e);
+            for (int i = 0; i < NE; ++i) {
+                qr[i] = repoll(qr[i], wq, g.qkv.p, (size_t)kh * SD + NE * j + i);
+                kr[i] = repoll(kr[i], wq, g.qkv.p, (size_t)key_dim + (size_t)kh * SD + NE * j + i);
             }
             ar = repoll(ar, wa, g.alpha.p, h);
             br = repoll(br, wb, g.beta.p, h);
         }
-        float qv[E], kv[E], qs = 0.f, ks = 0.f;
+        float qv[NE], kv[NE];
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            qv[e] = val(qr[e]);
-            kv[e] = val(kr[e]);
-            qs += qv[e] * qv[e];
-            ks += kv[e] * kv[e];
+        for (int i = 0; i < NE; ++i) {
+            qv[i] = val(qr[i]);
+            kv[i] = val(kr[i]);
         }
-        qs = wave_sum(qs);
-        ks = wave_sum(ks);
-        // q/k L2 normalisation (backend.cpp:30-35)
-        const float qscale = 1.f / sqrtf(qs + g.eps) / sqrtf((float)SD), kscale = 1.f / sqrtf(ks + g.eps);
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            qv[e] *= qscale;
-            kv[e] *= kscale;
-        }
+        gdn16_qk_norm<NE>(qv, kv, g.eps);  // q/k L2 normalisation (backend.cpp:30-35)
         const float decay = expf(gc(g.ssm_a)[h] * softplusf_(val(ar) + gc(g.dt)[h]));
         const float b = sigmoidf_(val(br));
-        const float v_lane = val(vr);
+        const float sum = gdn16_row<NE>(s, qv, kv, decay, b, val(vr));
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            float mem = 0.f;
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                s[r][e] *= decay;
-                mem += s[r][e] * kv[e];
-            }
-            mem = wave_sum(mem);
-            const float vd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v_lane), r));
-            const float delta = (vd - mem) * b;
-            float sum = 0.f;
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                s[r][e] += kv[e] * delta;
-                sum += s[r][e] * qv[e];
-            }
-            sum = wave_sum(sum);
-#pragma unroll
-            for (int e = 0; e < E; ++e) S[(size_t)(d0 + r) * SD + lane + 64 * e] = s[r][e];
-            if (lane == 0) st_out(g.out, (size_t)h * SD + d0 + r, sum, tag);
-        }
+        for (int i = 0; i < NE; ++i) Sd[i] = s[i];
+        if (j == 0) st_out(g.out, (size_t)h * SD + d, sum, tag);
     }
 }
 

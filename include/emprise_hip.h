@@ -175,8 +175,8 @@ emprise_status emprise_hip_quantize_q8(emprise_hip* h, emprise_dev x, int cols, 
 
 /* Backend::DeltaNet (backend.hpp:32-39) with device buffers. conv/ssm_a/dt/norm are
  * F32 vector weights; conv_state (channels*conv_width floats) and rec_state
- * (value_heads*state_dim*state_dim floats) are caller-owned device buffers that persist
- * across tokens. */
+ * (value_heads*state_dim*state_dim floats, 16-byte aligned: its rows move as 16-byte
+ * accesses) are caller-owned device buffers that persist across tokens. */
 typedef struct {
     int key_heads, value_heads, state_dim, conv_width;
     float eps;
