@@ -208,7 +208,7 @@ def test_delta_net_batch_matches_steps(backend, kh, vh, sd, cw, count):
     assert np.array_equal(backend.download(rows_d, count * W).reshape(count, W), rows)  # inputs untouched
 
 
-def test_delta_net_batch_rejects_bad_strides(backend):
+def test_delta_net_batch_rejects_bad_strides_and_state(backend):
     kh, vh, sd, cw = 4, 8, 64, 4
     kd, vd = kh * sd, vh * sd
     ch = 2 * kd + vd
@@ -220,6 +220,13 @@ def test_delta_net_batch_rejects_bad_strides(backend):
     for count, stride, out_stride in ((0, ch, vd), (2, ch - 1, vd), (2, ch, vd - 1), ((1 << 19) + 1, ch, vd)):
         with pytest.raises(InvalidArgument):
             backend.delta_net_batch(p, count, stride, out_stride)
+    # the recurrent state's rows move as 16-byte accesses: a state 4 bytes off is refused
+    # by every entry point that takes one, before anything runs
+    bad = DeltaNetParams(kh, vh, sd, cw, 1e-6, buf, buf, buf, buf, wconv, wa, wdt, wn, st, st + 4, buf)
+    for call in (lambda: backend.delta_net(bad), lambda: backend.delta_net_noalloc(bad),
+                 lambda: backend.delta_net_batch(bad, 2, ch, vd)):
+        with pytest.raises(InvalidArgument):
+            call()
 
 
 @pytest.mark.parametrize("H,kh,vh,sd,positions", [(512, 4, 8, 64, 40), (4096, 16, 32, 128, 2048)])
