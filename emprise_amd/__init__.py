@@ -85,6 +85,7 @@ def hip_lib() -> ctypes.CDLL:
         "emprise_hip_linear_batch": (st, [vp, u64, u64, u64, i32]),
         "emprise_hip_linear_batch_strided": (st, [vp, u64, u64, u64, u64, u64, i32]),
         "emprise_hip_linear_batch_many": (st, [vp, i32, vp, u64, u64, u64, u64, i32]),
+        "emprise_hip_ffn_gate_up_batch": (st, [vp, u64, u64, u64, u64, u64, u64, i32]),
         "emprise_hip_linear_norm": (st, [vp, vp, i32, P(u64), P(u64)]),
         "emprise_hip_feed_forward": (st, [vp, vp, u64, u64, u64, u64, u64]),
         "emprise_hip_ffn_gate_up": (st, [vp, vp, u64, u64, u64, u64]),
@@ -272,6 +273,9 @@ class HipBackend:
     def linear_batch_many(self, ws, X: int, ldx: int, Y: int, ldy: int, K: int):
         n = len(ws)
         self._check(self.lib.emprise_hip_linear_batch_many(self.h, n, (ctypes.c_uint64 * n)(*ws), X, ldx, Y, ldy, K))
+
+    def ffn_gate_up_batch(self, gate: int, up: int, X: int, ldx: int, Y: int, ldy: int, K: int):
+        self._check(self.lib.emprise_hip_ffn_gate_up_batch(self.h, gate, up, X, ldx, Y, ldy, K))
 
     def feed_forward(self, gate: int, up: int, down: int, x: int, y: int, inp: Input | None = None):
         self._check(self.lib.emprise_hip_feed_forward(self.h, ctypes.byref(inp) if inp else None, x, gate, up, down, y))

@@ -961,6 +961,56 @@ emprise_status emprise_hip_linear_batch_many(emprise_hip* h, int n, const empris
     return linear_batch_rows(h, n, ws, X, ldx, Y, ldy, K);
 }
 
+emprise_status emprise_hip_ffn_gate_up_batch(emprise_hip* h, emprise_weight gate, emprise_weight up, emprise_dev X,
+                                             uint64_t ldx, emprise_dev Y, uint64_t ldy, int K) {
+    if (!h || !X || !Y || K < 1) return fail(EMPRISE_EINVAL, "bad arguments");
+    const emprise_weight w[2] = {gate, up};
+    const Weight* ws[2];
+    TRY(check_weights(h, 2, w, ws));
+    const Weight *g = ws[0], *u = ws[1];
+    if (g->cols != u->cols || g->rows != u->rows) return fail(EMPRISE_EINVAL, "ffn_gate_up_batch: gate and up differ");
+    const int cols = (int)g->cols, F = (int)g->rows;
+    if (ldx < (uint64_t)cols || ldy < (uint64_t)F || ldx > (1u << 30) || ldy > (1u << 30) || 2ull * F > (1u << 30))
+        return fail(EMPRISE_EINVAL, "row strides shorter than the matrix");
+    float* y = reinterpret_cast<float*>(Y);
+    // gate and up of one chunked type: one GEMM over their interleaved rows, SwiGLU in its
+    // epilogue (gemm_q.hip, QGemmArgs::pair)
+    if ((g->type == kQ6K || g->type == kQ4K) && u->type == g->type && chunked_cols(g->cols) && K >= kGemmMinBatch &&
+        cols % 16 == 0 && X % 16 == 0 && ldx % 4 == 0) {
+        const bool sums = g->type == kQ4K;
+        QGemmArgs qa{};
+        void* xs;
+        TRY(h->get_scratch("gemm_xs", gemm_q16_split_bytes(K, cols, sums), &xs));
+        TRY(traced(h, "split_f16", (uint64_t)K * cols * 8, [&] {
+            return launch_gemm_q16_split(reinterpret_cast<const float*>(X), K, cols, (int)ldx, xs, sums, &qa, h->stream);
+        }));
+        qa.nseg = 2;
+        qa.w[0] = static_cast<const uint8_t*>(g->dev);
+        qa.w[1] = static_cast<const uint8_t*>(u->dev);
+        qa.row0[0] = 0;
+        qa.row0[1] = F;
+        qa.row0[2] = 2 * F;
+        qa.N = 2 * F;
+        qa.y = y;
+        qa.ldy = (int)ldy;
+        qa.pair = 1;
+        return traced(h, "gemm_q16", 4ull * K * cols * F, [&] { return launch_gemm_q16(g->type, qa, h->stream); });
+    }
+    // otherwise the two projections (gate into Y, up into scratch), then swiglu per row
+    void* ub;
+    TRY(h->get_scratch("ffn_up_batch", (size_t)K * F * sizeof(float), &ub));
+    TRY(linear_batch_rows(h, 1, &g, X, ldx, Y, ldy, K));
+    TRY(linear_batch_rows(h, 1, &u, X, ldx, reinterpret_cast<emprise_dev>(ub), (uint64_t)F, K));
+    for (int k0 = 0; k0 < K; k0 += 65535) {
+        const int n = std::min(65535, K - k0);
+        TRY(traced(h, "swiglu", (uint64_t)n * F * 12, [&] {
+            return launch_swiglu_rows(y + (size_t)k0 * ldy, ldy, static_cast<const float*>(ub) + (size_t)k0 * F, F, F, n,
+                                      h->stream);
+        }));
+    }
+    return EMPRISE_OK;
+}
+
 emprise_status emprise_hip_ffn_gate_up(emprise_hip* h, const emprise_hip_input* in, emprise_dev x, emprise_weight gate,
                                        emprise_weight up, emprise_dev hidden) {
     if (!h || !hidden || (!in && !x)) return fail(EMPRISE_EINVAL, "bad arguments");

@@ -183,10 +183,14 @@ __global__ __launch_bounds__(QThreads) void gemm_q16_kernel(QGemmArgs a) {
         const uint8_t* brow;  // (rows past N read row 0 and are zeroed)
         {
             const int r = b_ok ? bn : 0;
-            int sg = 0;
-            while (sg + 1 < a.nseg && r >= a.row0[sg + 1]) ++sg;
             constexpr size_t kChunk = T == kQ6K ? 3360 : 2304;
-            brow = a.w[sg] + (size_t)(r - a.row0[sg]) * cpr * kChunk;
+            if (a.pair) {
+                brow = a.w[r & 1] + (size_t)(r >> 1) * cpr * kChunk;
+            } else {
+                int sg = 0;
+                while (sg + 1 < a.nseg && r >= a.row0[sg + 1]) ++sg;
+                brow = a.w[sg] + (size_t)(r - a.row0[sg]) * cpr * kChunk;
+            }
         }
         // two register sets in turn (step k in set k%2): the loads of step k go out two
         // steps before it is stored; every load is issued whatever the step (past the last
@@ -400,17 +404,30 @@ __global__ __launch_bounds__(QThreads) void gemm_q16_kernel(QGemmArgs a) {
         __syncthreads();
     }
 
-    // Y[m][n] = 2^e_m * acc
+    // Y[m][n] = 2^e_m * acc. SwiGLU pairs: the gate (even n) and up (odd n) of one output sit
+    // in adjacent lanes; of accumulators r, r+1 (rows m, m+1) the even lane writes row m and
+    // the odd lane row m+1, each receiving the one value it lacks through a lane swap, so
+    // every lane evaluates one silu(gate) * up (swiglu_kernel's form) per two entries.
+    const bool odd = fr & 1;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             const int n = n0 + wn + 32 * nb + fr;
-            if (n >= a.N) continue;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
+            for (int r = 0; r < 16; r += 2) {
                 const int m = m0 + wm + 32 * mb + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-                if (m < a.M) a.y[(size_t)m * a.ldy + n] = ldexpf(acc[mb][nb][r], a.rexp[m]);
+                const float v0 = ldexpf(acc[mb][nb][r], a.rexp[min(m, a.M - 1)]);
+                const float v1 = ldexpf(acc[mb][nb][r + 1], a.rexp[min(m + 1, a.M - 1)]);
+                if (a.pair) {
+                    const float recv = dpp_f<0xb1, 0xf>(0.f, odd ? v0 : v1);  // quad_perm [1,0,3,2]
+                    const float gate = odd ? recv : v0, up = odd ? v1 : recv;
+                    const int mo = odd ? m + 1 : m;
+                    if (mo < a.M && n < a.N) a.y[(size_t)mo * a.ldy + (n >> 1)] = siluf_(gate) * up;
+                } else if (n < a.N) {
+                    if (m < a.M) a.y[(size_t)m * a.ldy + n] = v0;
+                    if (m + 1 < a.M) a.y[(size_t)(m + 1) * a.ldy + n] = v1;
+                }
             }
         }
 }
@@ -446,7 +463,9 @@ hipError_t launch_gemm_q16_split(const float* X, int M, int K, int ldx, void* sc
 
 hipError_t launch_gemm_q16(uint32_t type, const QGemmArgs& a, hipStream_t stream) {
     if ((type != kQ6K && type != kQ4K) || a.M < 1 || a.N < 1 || a.K % kChunkCols || a.nseg < 1 || a.nseg > kMaxSeg ||
-        a.row0[0] != 0 || a.row0[a.nseg] != a.N || a.ldy < a.N || (type == kQ4K && !a.sh))
+        a.row0[0] != 0 || a.row0[a.nseg] != a.N || (type == kQ4K && !a.sh))
+        return hipErrorInvalidValue;
+    if (a.pair ? (a.nseg != 2 || a.N % 2 || a.row0[1] * 2 != a.N || a.ldy < a.N / 2) : a.ldy < a.N)
         return hipErrorInvalidValue;
     const dim3 grid((a.N + QN - 1) / QN, (a.M + QM - 1) / QM);
     if (grid.y > 65535) return hipErrorInvalidValue;

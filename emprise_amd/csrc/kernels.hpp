@@ -124,6 +124,9 @@ struct QGemmArgs {
     int nseg, N;
     float* y;
     int ldy;
+    // SwiGLU pairs: two segments of N/2 rows each (gate, up), interleaved -- GEMM row n is
+    // row n/2 of segment n%2 -- and y[m][n/2] = silu(gate) * up in place of both rows
+    int pair;
 };
 size_t gemm_q16_split_bytes(int M, int K, bool sums);
 hipError_t launch_gemm_q16_split(const float* X, int M, int K, int ldx, void* scratch, bool sums, QGemmArgs* a,
@@ -231,6 +234,8 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int n
                                hipStream_t stream);
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream);
 hipError_t launch_swiglu(float* gate, const float* up, int n, hipStream_t stream);
+hipError_t launch_swiglu_rows(float* gate, size_t ldg, const float* up, size_t ldu, int n, int rows,
+                              hipStream_t stream);
 hipError_t launch_embed(const uint8_t* w, uint32_t type, int cols, int rows, const int* token, float* out,
                         hipStream_t stream);
 hipError_t launch_embed_rows(const uint8_t* w, uint32_t type, int cols, int rows, const int* tokens, int count,

@@ -40,6 +40,13 @@ __global__ void swiglu_kernel(float* gate, const float* up, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) gate[i] = siluf_(gate[i]) * up[i];
 }
+// swiglu over `rows` rows of n: row r of gate at r * ldg, of up at r * ldu
+__global__ void swiglu_rows_kernel(float* gate, size_t ldg, const float* up, size_t ldu, int n, int rows) {
+    const int r = blockIdx.y;
+    if (r >= rows) return;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        gate[(size_t)r * ldg + i] = siluf_(gate[(size_t)r * ldg + i]) * up[(size_t)r * ldu + i];
+}
 
 // row blockIdx.y of out = embedding row token[blockIdx.y]
 __global__ void embed_kernel(const uint8_t* w, uint32_t type, int cols, int rows, const int* token, float* out) {
@@ -134,6 +141,13 @@ hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream) {
 }
 hipError_t launch_swiglu(float* gate, const float* up, int n, hipStream_t stream) {
     launch_kernel(swiglu_kernel, dim3(grid_for((size_t)n, 256, 1u << 20)), dim3(256), 0, stream, gate, up, n);
+    return hipGetLastError();
+}
+hipError_t launch_swiglu_rows(float* gate, size_t ldg, const float* up, size_t ldu, int n, int rows,
+                              hipStream_t stream) {
+    if (rows < 1 || rows > 65535 || n < 1) return hipErrorInvalidValue;
+    launch_kernel(swiglu_rows_kernel, dim3(grid_for((size_t)n, 256, 64), rows), dim3(256), 0, stream, gate, ldg, up,
+                  ldu, n, rows);
     return hipGetLastError();
 }
 hipError_t launch_embed(const uint8_t* w, uint32_t type, int cols, int rows, const int* token, float* out,

@@ -84,6 +84,10 @@ public:
         hip_check(emprise_hip_linear_batch_many(h_, static_cast<int>(w.size()), w.data(), x, ldx, y, ldy, k),
                   "linear_batch_many");
     }
+    void dev_ffn_gate_up_batch(emprise_weight gate, emprise_weight up, emprise_dev x, uint64_t ldx, emprise_dev y,
+                               uint64_t ldy, int k) {
+        hip_check(emprise_hip_ffn_gate_up_batch(h_, gate, up, x, ldx, y, ldy, k), "ffn_gate_up_batch");
+    }
     void dev_swiglu(emprise_dev gate, emprise_dev up, int n) { hip_check(emprise_hip_swiglu(h_, gate, up, n), "swiglu"); }
     void dev_delta_net(const emprise_hip_delta_net_params& p) { hip_check(emprise_hip_delta_net(h_, &p), "delta_net"); }
     void dev_delta_net_batch(const emprise_hip_delta_net_params& p, int count, uint64_t stride, uint64_t out_stride) {

@@ -600,9 +600,7 @@ void Model::prefill_batched(size_t start, size_t count, std::vector<float>* logi
             }
             b.dev_add(pf_x_, pf_c_, static_cast<int>(T * H));
             b.dev_rmsnorm_rows(pf_x_, L.post_norm, pf_xn_, static_cast<int>(H), T, d.eps);
-            b.dev_linear_batch(L.gate, pf_xn_, H, pf_a_, F, T);
-            b.dev_linear_batch(L.up, pf_xn_, H, pf_b_, F, T);
-            b.dev_swiglu(pf_a_, pf_b_, static_cast<int>(T * F));
+            b.dev_ffn_gate_up_batch(L.gate, L.up, pf_xn_, H, pf_a_, F, T);
             b.dev_linear_batch(L.down, pf_a_, F, pf_c_, H, T);
             b.dev_add(pf_x_, pf_c_, static_cast<int>(T * H));
         }

@@ -119,6 +119,14 @@ emprise_status emprise_hip_linear_batch_strided(emprise_hip* h, emprise_weight w
  * the prefill). Batched prefill support, like linear_batch_strided. */
 emprise_status emprise_hip_linear_batch_many(emprise_hip* h, int n, const emprise_weight* w, emprise_dev X,
                                              uint64_t ldx, emprise_dev Y, uint64_t ldy, int K);
+/* The gate/up half of Backend::feed_forward (backend.hpp:27-28; the reference's fused FFN,
+ * model.cpp:230-236, swiglu at cuda.cpp:560-566) over K inputs: Y[k] = silu(G X[k]) * (U X[k]),
+ * F = rows of G = rows of U floats per row, strides in floats. Chunked Q6_K/Q4_K gate and
+ * up of one type run as one GEMM whose epilogue forms the SwiGLU; the values are those of
+ * linear_batch_strided for G and U followed by swiglu, bit for bit. Batched prefill
+ * support, like linear_batch_strided. */
+emprise_status emprise_hip_ffn_gate_up_batch(emprise_hip* h, emprise_weight gate, emprise_weight up, emprise_dev X,
+                                             uint64_t ldx, emprise_dev Y, uint64_t ldy, int K);
 
 /* Input transform fused into a projection's prologue. It stands for the reference's
  * dev_add + dev_rmsnorm pair in front of every projection group (model.cpp:429,

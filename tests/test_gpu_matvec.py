@@ -129,6 +129,49 @@ def test_linear_batch_wide_range(backend, wtype):
     backend.weight_free(w)
 
 
+# (type, K, F, cols, ldy pad): the paired GEMM (8+ tokens, chunked Q6_K/Q4_K), tile-ragged
+# token and row counts, the 9B FFN shape; fewer than 8 tokens and F32 weights take the
+# two-projection path
+@pytest.mark.parametrize("wtype,K,F,cols,pad", [(Q6_K, 8, 1000, 4096, 0), (Q4_K, 129, 1000, 4096, 3),
+                                                (Q6_K, 200, 12288, 4096, 0), (Q4_K, 300, 64, 8192, 5),
+                                                (Q6_K, 3, 700, 4096, 1), (F32, 40, 96, 512, 2)])
+def test_ffn_gate_up_batch(backend, wtype, K, F, cols, pad):
+    """emprise_hip_ffn_gate_up_batch: Y[k] = silu(G X[k]) * (U X[k]) equals the two
+    projections of linear_batch_strided followed by swiglu, bit for bit (the paired
+    GEMM interleaves gate and up rows and forms the SwiGLU in its epilogue), and the
+    per-op bar against the CPU matvecs for the first and last token."""
+    rng = np.random.default_rng(K * 7 + F + wtype)
+    if wtype == F32:
+        rg = rng.standard_normal((F, cols)).astype(np.float32) * 0.05
+        ru = rng.standard_normal((F, cols)).astype(np.float32) * 0.05
+        g = backend.upload_weight(F32, cols, F, rg.tobytes())
+        u = backend.upload_weight(F32, cols, F, ru.tobytes())
+    else:
+        rg, ru = matrix(rng, wtype, F, cols), matrix(rng, wtype, F, cols)
+        g, u = backend.upload_weight(wtype, cols, F, rg), backend.upload_weight(wtype, cols, F, ru)
+    X = rng.standard_normal((K, cols)).astype(np.float32)
+    ldy = F + pad
+    xd, yd = backend.to_device(X), backend.alloc(K * ldy * 4)
+    backend.ffn_gate_up_batch(g, u, xd, cols, yd, ldy, K)
+    Y = backend.download(yd, (K, ldy))[:, :F]
+    gd, ud = backend.alloc(K * F * 4), backend.alloc(K * F * 4)
+    backend.linear_batch_strided(g, xd, cols, gd, F, K)
+    backend.linear_batch_strided(u, xd, cols, ud, F, K)
+    backend.swiglu(gd, ud, K * F)
+    assert np.array_equal(Y, backend.download(gd, (K, F)))
+    for k in (0, K - 1):
+        if wtype == F32:
+            gr, ur = rg @ X[k], ru @ X[k]
+        else:
+            gr, ur = oracle.matvec(wtype, rg, X[k], F), oracle.matvec(wtype, ru, X[k], F)
+        ref = (gr / (1 + np.exp(-gr.astype(np.float64))) * ur).astype(np.float32)
+        _close(Y[k], ref)
+    for b in (xd, yd, gd, ud):
+        backend.free(b)
+    backend.weight_free(g)
+    backend.weight_free(u)
+
+
 @pytest.mark.parametrize("K", [3, 40])
 def test_linear_batch_strided(backend, K):
     """Strided batched projection writes its rows into a slice of wider output rows."""
