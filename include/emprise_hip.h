@@ -211,10 +211,8 @@ emprise_status emprise_hip_delta_net_noalloc(emprise_hip* h, const emprise_hip_d
  * (the reference runs it position by position inside its 4-position prefill batches,
  * model.cpp:355-366): qkv, gate, alpha and beta are the rows of position 0, the rows of
  * position t are `stride` floats further; out receives `count` rows `out_stride` floats
- * apart. Per position the same arithmetic as emprise_hip_delta_net (the conv history
- * bit for bit); each state row's dot products are summed in another order (over 16
- * lanes instead of 64), so outputs and final states agree with `count` calls of it to
- * FP32 rounding, not bit for bit. qkv is not modified.
+ * apart. Per position the same arithmetic, in the same order, as emprise_hip_delta_net,
+ * so outputs and final states equal `count` calls of it. qkv is not modified.
  * 1 <= count <= 524288. */
 emprise_status emprise_hip_delta_net_batch(emprise_hip* h, const emprise_hip_delta_net_params* p, int count,
                                            uint64_t stride, uint64_t out_stride);
