@@ -67,6 +67,33 @@ __device__ __forceinline__ int attn_per(int len) {
     return (nsub + kAttnSplit - 1) / kAttnSplit;
 }
 
+// Eight wave-wide sums at once: halving exchanges across lanes l^32 and l^16
+// (v_permlane32_swap / v_permlane16_swap, each pair of values trading the halves the
+// other lane keeps) and l^8 (a row rotation) leave lane l with value
+// (l>>3 & 1) + 2*(l>>4 & 1) + 4*(l>>5 & 1) summed over 8 lanes, and a three-step butterfly
+// inside each group of 8 lanes completes it (the same bits in all 8); value j is then
+// read from lane 8j. About half the instructions of eight wave_sum, and a shorter chain.
+__device__ __forceinline__ void wave_sum8(const float (&x)[8], float (&out)[8]) {
+    float y[4], z[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[j]), __float_as_uint(x[j + 4]), false, false);
+        y[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // lanes 0-31: value j, 32-63: value j+4
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(y[j]), __float_as_uint(y[j + 2]), false, false);
+        z[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // even rows of 16: slot j, odd rows: slot j+2
+    }
+    const bool hi8 = (threadIdx.x & 8) != 0;
+    float w = (hi8 ? z[1] : z[0]) + dpp_f<0x128, 0xf>(0.f, hi8 ? z[0] : z[1]);  // row_ror:8
+    w += dpp_f<0xb1, 0xf>(0.f, w);   // quad_perm [1,0,3,2]
+    w += dpp_f<0x4e, 0xf>(0.f, w);   // quad_perm [2,3,0,1]
+    w += dpp_f<0x141, 0xf>(0.f, w);  // row_half_mirror
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 8 * j));
+}
+
 template <int E>  // head_dim = 64 * E
 __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) {
     constexpr int HD = 64 * E, CH = kAttnSub, PW = CH / kAttnWaves;  // rows per wave and sub-chunk
@@ -197,15 +224,36 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
                 ldv<E>(kr[i], knew + E * lane);
                 ldv<E>(vr[i], vnew + E * lane);
             }
+        }
+        if (PW * 4 == 8 && group == 4) {
+            // the wave's eight scores (PW rows x 4 heads) reduced together
+            float d[8], s8[8];
 #pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
-                if (g < group) {
-                    float d = 0.f;
+            for (int i = 0; i < PW; ++i)
 #pragma unroll
-                    for (int e = 0; e < E; ++e) d = fmaf(qv[g][e], kr[i][e], d);
-                    sc[i][g] = wave_sum(d) * inv_root;
+                for (int g = 0; g < 4; ++g) {
+                    float p = 0.f;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) p = fmaf(qv[g][e], kr[i][e], p);
+                    d[(4 * i + g) & 7] = p;
                 }
-            }
+            wave_sum8(d, s8);
+#pragma unroll
+            for (int i = 0; i < PW; ++i)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) sc[i][g] = s8[(4 * i + g) & 7] * inv_root;
+        } else {
+#pragma unroll
+            for (int i = 0; i < PW; ++i)
+#pragma unroll
+                for (int g = 0; g < kMaxGroup; ++g) {
+                    if (g < group) {
+                        float p = 0.f;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) p = fmaf(qv[g][e], kr[i][e], p);
+                        sc[i][g] = wave_sum(p) * inv_root;
+                    }
+                }
         }
 #pragma unroll
         for (int g = 0; g < kMaxGroup; ++g) {
