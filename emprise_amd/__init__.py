@@ -91,6 +91,7 @@ def hip_lib() -> ctypes.CDLL:
         "emprise_hip_ffn_gate_up": (st, [vp, vp, u64, u64, u64, u64]),
         "emprise_hip_rmsnorm": (st, [vp, u64, u64, u64, i32, f32]),
         "emprise_hip_rmsnorm_rows": (st, [vp, u64, u64, u64, i32, i32, f32]),
+        "emprise_hip_add_rmsnorm_rows": (st, [vp, u64, u64, u64, u64, i32, i32, f32]),
         "emprise_hip_add": (st, [vp, u64, u64, i32]),
         "emprise_hip_swiglu": (st, [vp, u64, u64, i32]),
         "emprise_hip_embed": (st, [vp, u64, u64, u64]),
@@ -288,6 +289,9 @@ class HipBackend:
 
     def rmsnorm_rows(self, x: int, w: int, out: int, n: int, rows: int, eps: float):
         self._check(self.lib.emprise_hip_rmsnorm_rows(self.h, x, w, out, n, rows, eps))
+
+    def add_rmsnorm_rows(self, x: int, delta: int, w: int, out: int, n: int, rows: int, eps: float):
+        self._check(self.lib.emprise_hip_add_rmsnorm_rows(self.h, x, delta, w, out, n, rows, eps))
 
     def add(self, x: int, y: int, n: int):
         self._check(self.lib.emprise_hip_add(self.h, x, y, n))

@@ -1061,6 +1061,19 @@ emprise_status emprise_hip_rmsnorm_rows(emprise_hip* h, emprise_dev x, emprise_w
     });
 }
 
+emprise_status emprise_hip_add_rmsnorm_rows(emprise_hip* h, emprise_dev x, emprise_dev delta, emprise_weight w,
+                                           emprise_dev out, int n, int rows, float eps) {
+    const Weight* wt = h ? h->weight(w) : nullptr;
+    if (!wt || !x || !delta || !out || n < 1 || rows < 1) return fail(EMPRISE_EINVAL, "bad arguments");
+    if (wt->type != kF32 || wt->rows * wt->cols != (uint64_t)n) return fail(EMPRISE_EINVAL, "RMS normalization dimensions");
+    if (out == x || out == delta) return fail(EMPRISE_EINVAL, "out aliases an input");
+    return traced(h, "add_rmsnorm", (uint64_t)n * rows * 16 + (uint64_t)n * 4, [&] {
+        return launch_add_rmsnorm_rows(reinterpret_cast<float*>(x), reinterpret_cast<const float*>(delta),
+                                       reinterpret_cast<const float*>(wt->dev), reinterpret_cast<float*>(out), n, rows,
+                                       eps, h->stream);
+    });
+}
+
 emprise_status emprise_hip_embed_rows(emprise_hip* h, emprise_weight embedding, emprise_dev tokens, int count,
                                       emprise_dev out) {
     const Weight* w = h ? h->weight(embedding) : nullptr;

@@ -232,6 +232,8 @@ hipError_t launch_fill_u64(unsigned long long* dst, unsigned long long value, si
 hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t stream);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int n, int rows, float eps,
                                hipStream_t stream);
+hipError_t launch_add_rmsnorm_rows(float* x, const float* delta, const float* w, float* out, int n, int rows, float eps,
+                                  hipStream_t stream);
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream);
 hipError_t launch_swiglu(float* gate, const float* up, int n, hipStream_t stream);
 hipError_t launch_swiglu_rows(float* gate, size_t ldg, const float* up, size_t ldu, int n, int rows,

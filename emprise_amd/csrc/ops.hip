@@ -30,6 +30,25 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const flo
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * (scale * w[i]);
 }
 
+// add_kernel then rmsnorm_kernel on row r in one pass: x += delta, out = rms(x) * w, the
+// same values and the same sum order as the two kernels
+__global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* x, const float* delta, const float* w, float* out,
+                                                           int n, float eps) {
+    __shared__ float red[16];
+    x += (size_t)blockIdx.x * n;
+    delta += (size_t)blockIdx.x * n;
+    out += (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i] + delta[i];
+        x[i] = v;
+        ss += v * v;
+    }
+    const float total = block_sum(ss, red);
+    const float scale = 1.f / sqrtf(total / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * (scale * w[i]);
+}
+
 __global__ void add_kernel(float* x, const float* y, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) x[i] += y[i];
@@ -133,6 +152,12 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int n
                                hipStream_t stream) {
     if (rows < 1) return hipErrorInvalidValue;
     launch_kernel(rmsnorm_kernel, dim3(rows), dim3(1024), 0, stream, x, w, out, n, eps);
+    return hipGetLastError();
+}
+hipError_t launch_add_rmsnorm_rows(float* x, const float* delta, const float* w, float* out, int n, int rows, float eps,
+                                  hipStream_t stream) {
+    if (rows < 1) return hipErrorInvalidValue;
+    launch_kernel(add_rmsnorm_kernel, dim3(rows), dim3(1024), 0, stream, x, delta, w, out, n, eps);
     return hipGetLastError();
 }
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream) {

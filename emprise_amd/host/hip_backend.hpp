@@ -75,6 +75,10 @@ public:
     void dev_rmsnorm_rows(emprise_dev x, emprise_weight w, emprise_dev out, int n, int rows, float eps) {
         hip_check(emprise_hip_rmsnorm_rows(h_, x, w, out, n, rows, eps), "rmsnorm_rows");
     }
+    void dev_add_rmsnorm_rows(emprise_dev x, emprise_dev delta, emprise_weight w, emprise_dev out, int n, int rows,
+                              float eps) {
+        hip_check(emprise_hip_add_rmsnorm_rows(h_, x, delta, w, out, n, rows, eps), "add_rmsnorm_rows");
+    }
     void dev_linear_batch(emprise_weight w, emprise_dev x, uint64_t ldx, emprise_dev y, uint64_t ldy, int k) {
         hip_check(emprise_hip_linear_batch_strided(h_, w, x, ldx, y, ldy, k), "linear_batch");
     }

@@ -556,8 +556,15 @@ void Model::prefill_batched(size_t start, size_t count, std::vector<float>* logi
     for (size_t p0 = 0; p0 < count; p0 += rows) {
         const int T = static_cast<int>(std::min(rows, count - p0));
         b.dev_embed_rows(embd_, dev_prompt_ + (start + p0) * sizeof(int), T, pf_x_);
+        // each residual add (model.cpp:226, :243) runs in the pass of the RMSNorm after it
+        bool pending = false;  // pf_c_ holds a delta not yet added to pf_x_
+        auto norm_rows = [&](emprise_weight w) {
+            if (pending) b.dev_add_rmsnorm_rows(pf_x_, pf_c_, w, pf_xn_, static_cast<int>(H), T, d.eps);
+            else b.dev_rmsnorm_rows(pf_x_, w, pf_xn_, static_cast<int>(H), T, d.eps);
+            pending = false;
+        };
         for (const Layer& L : layers_) {
-            b.dev_rmsnorm_rows(pf_x_, L.attn_norm, pf_xn_, static_cast<int>(H), T, d.eps);
+            norm_rows(L.attn_norm);
             if (L.recurrent) {
                 const uint64_t W = ch + vd + 2 * vh;
                 b.dev_linear_batch_many({L.qkv, L.zgate, L.alpha, L.beta}, pf_xn_, H, pf_a_, W, T);
@@ -598,10 +605,15 @@ void Model::prefill_batched(size_t start, size_t count, std::vector<float>* logi
                 b.dev_attention_batch(p, pf_a_, T, W, static_cast<int>(start + p0), pf_b_, ao);
                 b.dev_linear_batch(L.o, pf_b_, ao, pf_c_, H, T);
             }
-            b.dev_add(pf_x_, pf_c_, static_cast<int>(T * H));
-            b.dev_rmsnorm_rows(pf_x_, L.post_norm, pf_xn_, static_cast<int>(H), T, d.eps);
+            pending = true;
+            norm_rows(L.post_norm);
             b.dev_ffn_gate_up_batch(L.gate, L.up, pf_xn_, H, pf_a_, F, T);
             b.dev_linear_batch(L.down, pf_a_, F, pf_c_, H, T);
+            pending = true;
+        }
+        if (logits) {
+            norm_rows(output_norm_);
+        } else if (pending) {
             b.dev_add(pf_x_, pf_c_, static_cast<int>(T * H));
         }
         if (logits) {
@@ -609,7 +621,6 @@ void Model::prefill_batched(size_t start, size_t count, std::vector<float>* logi
             constexpr int kHeadRows = 64;
             const uint64_t V = static_cast<uint64_t>(d.vocab);
             if (!pf_logits_) pf_logits_ = b.dev_alloc(kHeadRows * V * 4);
-            b.dev_rmsnorm_rows(pf_x_, output_norm_, pf_xn_, static_cast<int>(H), T, d.eps);
             for (int r0 = 0; r0 < T; r0 += kHeadRows) {
                 const int n = std::min(kHeadRows, T - r0);
                 b.dev_linear_batch(output_, pf_xn_ + static_cast<uint64_t>(r0) * H * 4, H, pf_logits_, V, n);

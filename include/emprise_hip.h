@@ -161,6 +161,12 @@ emprise_status emprise_hip_rmsnorm(emprise_hip* h, emprise_dev x, emprise_weight
 /* dev_rmsnorm over `rows` consecutive rows of n floats (batched prefill). */
 emprise_status emprise_hip_rmsnorm_rows(emprise_hip* h, emprise_dev x, emprise_weight w, emprise_dev out, int n,
                                        int rows, float eps);
+/* dev_add then dev_rmsnorm (backend.hpp:64-65; model.cpp:226-228, :243-249) over `rows`
+ * rows in one pass: x += delta, out = rms(x) * w; the results of emprise_hip_add followed
+ * by emprise_hip_rmsnorm_rows, bit for bit. out must not alias x or delta. Batched
+ * prefill support. */
+emprise_status emprise_hip_add_rmsnorm_rows(emprise_hip* h, emprise_dev x, emprise_dev delta, emprise_weight w,
+                                           emprise_dev out, int n, int rows, float eps);
 /* Backend::dev_add (backend.hpp:65), add_inplace cuda.cpp:543-546: x += y. */
 emprise_status emprise_hip_add(emprise_hip* h, emprise_dev x, emprise_dev y, int n);
 /* swiglu, cuda.cpp:560-566: gate = silu(gate) * up. */

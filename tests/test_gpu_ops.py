@@ -39,7 +39,19 @@ def test_rmsnorm_rows_and_embed_rows(backend):
     td, ed = backend.to_device(toks), backend.alloc(len(toks) * cols * 4)
     backend.embed_rows(emb, td, len(toks), ed)
     assert np.array_equal(backend.download(ed, (len(toks), cols)), table[toks])
-    for b in (xd, od, td, ed):
+    # the residual add fused into the norm's pass: x and out bit-equal to add + rmsnorm_rows
+    delta = rng.standard_normal((rows, n)).astype(np.float32)
+    x2, dd, o2 = backend.to_device(x), backend.to_device(delta), backend.alloc(rows * n * 4)
+    backend.add_rmsnorm_rows(x2, dd, wd, o2, n, rows, 1e-6)
+    x3 = backend.to_device(x)
+    backend.add(x3, dd, rows * n)
+    backend.rmsnorm_rows(x3, wd, od, n, rows, 1e-6)
+    assert np.array_equal(backend.download(x2, (rows, n)), x + delta)
+    assert np.array_equal(backend.download(x2, (rows, n)), backend.download(x3, (rows, n)))
+    assert np.array_equal(backend.download(o2, (rows, n)), backend.download(od, (rows, n)))
+    with pytest.raises(InvalidArgument):
+        backend.add_rmsnorm_rows(x2, dd, wd, x2, n, rows, 1e-6)  # out aliasing x
+    for b in (xd, od, td, ed, x2, dd, o2, x3):
         backend.free(b)
     backend.weight_free(emb)
     backend.weight_free(wd)
