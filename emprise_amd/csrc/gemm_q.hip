@@ -112,6 +112,78 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
     }
 }
 
+// The same split for 16-byte aligned rows of P * 2048 columns: lane t of pass p holds
+// columns 8(256p + t) .. +7 in registers from the row maximum to the stores (two 16-byte
+// loads, one 16-byte store per piece), and a Q4_K unit's 32 columns are a DPP quad: each
+// lane sums its 8 values in column order, the quad adds the pairs (s0 + s1) + (s2 + s3).
+template <int P>
+__global__ __launch_bounds__(256) void split_rows8_kernel(const float* __restrict__ X, int M, int K, int ldx,
+                                                          _Float16* __restrict__ xh, _Float16* __restrict__ xl,
+                                                          int* __restrict__ rexp, _Float16* __restrict__ sh,
+                                                          _Float16* __restrict__ sl) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __shared__ float red[4];
+    const int m = blockIdx.x, t = threadIdx.x;
+    if (m >= M) {  // padding rows of the last tile
+        const half8 z = {};
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const size_t o = tiled(m, 8 * (256 * p + t), K);
+            *reinterpret_cast<half8*>(xh + o) = z;
+            *reinterpret_cast<half8*>(xl + o) = z;
+        }
+        return;
+    }
+    const float* x = X + (size_t)m * ldx;
+    f4v v[P][2];
+    float mx = 0.f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const f4v* src = reinterpret_cast<const f4v*>(x + 8 * (256 * p + t));
+        v[p][0] = src[0];
+        v[p][1] = src[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fmaxf(fabsf(v[p][0][i]), fabsf(v[p][1][i])));
+    }
+    mx = wave_max(mx);
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (mx > 0.f && mx < INFINITY) {
+        (void)frexpf(mx, &e);  // mx = f * 2^e with f in [0.5, 1)
+        e -= 1;                // mx * 2^-e in [1, 2)
+    }
+    if (t == 0) rexp[m] = e;
+    const int units = K / 32;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        half8 h8, l8;
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float w = ldexpf(v[p][i >> 2][i & 3], -e);
+            const _Float16 h = (_Float16)w;
+            h8[i] = h;
+            l8[i] = (_Float16)(w - (float)h);
+            s += w;
+        }
+        const size_t o = tiled(m, 8 * (256 * p + t), K);
+        *reinterpret_cast<half8*>(xh + o) = h8;
+        *reinterpret_cast<half8*>(xl + o) = l8;
+        if (sh) {
+            s += dpp_f<0xb1, 0xf>(0.f, s);  // quad_perm [1,0,3,2]: s0 + s1, s2 + s3
+            s += dpp_f<0x4e, 0xf>(0.f, s);  // quad_perm [2,3,0,1]
+            if ((t & 3) == 0) {
+                const int u = (256 * p + t) >> 2;
+                const _Float16 h = (_Float16)s;
+                sh[(size_t)m * units + u] = h;
+                sl[(size_t)m * units + u] = (_Float16)(s - (float)h);
+            }
+        }
+    }
+}
+
 // ---- the GEMM ------------------------------------------------------------------------
 
 template <int T> struct QRaw;
@@ -450,7 +522,15 @@ hipError_t launch_gemm_q16_split(const float* X, int M, int K, int ldx, void* sc
     int* rexp = reinterpret_cast<int*>(xl + (size_t)mp * K);
     _Float16* sh = sums ? reinterpret_cast<_Float16*>(rexp + M) : nullptr;
     _Float16* sl = sums ? sh + (size_t)M * (K / 32) : nullptr;
-    launch_kernel(split_rows_kernel, dim3(mp), dim3(256), 0, stream, X, M, K, ldx, xh, xl, rexp, sh, sl);
+    const bool v16 = reinterpret_cast<uintptr_t>(X) % 16 == 0 && ldx % 4 == 0;
+    if (v16 && K == 4096)
+        launch_kernel(split_rows8_kernel<2>, dim3(mp), dim3(256), 0, stream, X, M, K, ldx, xh, xl, rexp, sh, sl);
+    else if (v16 && K == 8192)
+        launch_kernel(split_rows8_kernel<4>, dim3(mp), dim3(256), 0, stream, X, M, K, ldx, xh, xl, rexp, sh, sl);
+    else if (v16 && K == 12288)
+        launch_kernel(split_rows8_kernel<6>, dim3(mp), dim3(256), 0, stream, X, M, K, ldx, xh, xl, rexp, sh, sl);
+    else
+        launch_kernel(split_rows_kernel, dim3(mp), dim3(256), 0, stream, X, M, K, ldx, xh, xl, rexp, sh, sl);
     a->xh = reinterpret_cast<const uint16_t*>(xh);
     a->xl = reinterpret_cast<const uint16_t*>(xl);
     a->rexp = rexp;
