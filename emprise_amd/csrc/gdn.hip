@@ -298,21 +298,29 @@ __global__ __launch_bounds__(kScanWaves * 64) void gdn_scan_kernel(GdnBatchArgs 
     for (int t0 = 0, buf = 0; t0 < a.count; t0 += kScanBlock, buf ^= 1) {
         lane_load(t0 + kScanBlock, nxt);
         // positions t0 + 16q .. +15
+        // a position's q|k from LDS, read one position ahead of its use
+        auto lds_qk = [&](int u, float (&qv)[NE], float (&kv)[NE]) {
+#pragma unroll
+            for (int c = 0; c < NC / 2; ++c) {
+                const float4 x = *reinterpret_cast<const float4*>(&qks[buf][u][(c * 16 + j) * 4]);
+                const float4 y = *reinterpret_cast<const float4*>(&qks[buf][u][((c + NC / 2) * 16 + j) * 4]);
+                qv[4 * c] = x.x, qv[4 * c + 1] = x.y, qv[4 * c + 2] = x.z, qv[4 * c + 3] = x.w;
+                kv[4 * c] = y.x, kv[4 * c + 1] = y.y, kv[4 * c + 2] = y.z, kv[4 * c + 3] = y.w;
+            }
+        };
         auto group = [&](auto qc) {
             constexpr int q = decltype(qc)::value;
             float ol = 0.f;
+            float qn[NE], kn[NE];
+            lds_qk(16 * q, qn, kn);
             static_for<16>([&](auto uc) {
                 constexpr int uu = decltype(uc)::value;
                 const int u = 16 * q + uu;
                 {
                     float qv[NE], kv[NE];
 #pragma unroll
-                    for (int c = 0; c < NC / 2; ++c) {
-                        const float4 x = *reinterpret_cast<const float4*>(&qks[buf][u][(c * 16 + j) * 4]);
-                        const float4 y = *reinterpret_cast<const float4*>(&qks[buf][u][((c + NC / 2) * 16 + j) * 4]);
-                        qv[4 * c] = x.x, qv[4 * c + 1] = x.y, qv[4 * c + 2] = x.z, qv[4 * c + 3] = x.w;
-                        kv[4 * c] = y.x, kv[4 * c + 1] = y.y, kv[4 * c + 2] = y.z, kv[4 * c + 3] = y.w;
-                    }
+                    for (int e = 0; e < NE; ++e) qv[e] = qn[e], kv[e] = kn[e];
+                    if constexpr (uu + 1 < 16) lds_qk(u + 1, qn, kn);
                     const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.dg.x), u));
                     const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.dg.y), u));
                     const float vd = row16_bcast<uu>(cur.v[q]);
