@@ -488,6 +488,49 @@ __global__ __launch_bounds__(256) void attn_softmax_batch_kernel(AttnBatchArgs a
     for (int j = threadIdx.x; j < a.lp; j += blockDim.x) s[j] = j < n ? s[j] / total : 0.f;
 }
 
+// The same row softmax for rows of at most 256 * KR keys, the row held in registers from
+// its one read to its one write (the same thread-to-key assignment and sums as above,
+// so the same results).
+template <int KR>
+__global__ __launch_bounds__(256) void attn_softmax_rows_kernel(AttnBatchArgs a) {
+    __shared__ float red[8];
+    const int row = blockIdx.x;  // h * count + t
+    const int t = row % a.count;
+    const int n = a.first + t + 1;
+    float* s = a.scores + (size_t)row * a.lp;
+    const float root = sqrtf((float)a.head_dim);
+    float v[KR];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+        const int j = threadIdx.x + 256 * k;
+        v[k] = j < n ? s[j] / root : -INFINITY;
+        m = fmaxf(m, v[k]);
+    }
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+        if ((int)threadIdx.x + 256 * k < n) {
+            v[k] = expf(v[k] - m);
+            total += v[k];
+        }
+    }
+    total = wave_sum(total);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = total;
+    __syncthreads();
+    total = (red[0] + red[1]) + (red[2] + red[3]);
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+        const int j = threadIdx.x + 256 * k;
+        if (j < a.lp) s[j] = j < n ? v[k] / total : 0.f;
+    }
+}
+
 // vt[kvh][d][j] = values[j][kvh][d] for keys j < L, 0 up to lp: 32 x 32 tiles via LDS.
 __global__ __launch_bounds__(256) void attn_vt_batch_kernel(AttnBatchArgs a) {
     __shared__ float tile[32][33];
@@ -533,7 +576,12 @@ hipError_t launch_attention_batch(const AttnBatchArgs& a, hipStream_t stream) {
     e = launch_gemm_f32_heads(a.q, a.keys, a.scores, a.count, L, hd, a.heads * hd, kvd, a.lp, a.heads, group,
                               (size_t)hd, (size_t)hd, (size_t)a.count * a.lp, true, false, a.first, stream);
     if (e != hipSuccess) return e;
-    launch_kernel(attn_softmax_batch_kernel, dim3(a.heads * a.count), dim3(256), 0, stream, a);
+    if (a.lp <= 256 * 8)
+        launch_kernel(attn_softmax_rows_kernel<8>, dim3(a.heads * a.count), dim3(256), 0, stream, a);
+    else if (a.lp <= 256 * 16)
+        launch_kernel(attn_softmax_rows_kernel<16>, dim3(a.heads * a.count), dim3(256), 0, stream, a);
+    else
+        launch_kernel(attn_softmax_batch_kernel, dim3(a.heads * a.count), dim3(256), 0, stream, a);
     launch_kernel(attn_vt_batch_kernel, dim3(a.lp / 32, hd / 32, a.kv_heads), dim3(256), 0, stream, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
