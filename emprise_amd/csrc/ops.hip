@@ -49,6 +49,35 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* x, const float
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * (scale * w[i]);
 }
 
+// The same for rows of at most 1024 * KR values, each sum x + delta kept in registers
+// for the second pass instead of read back (same element-to-thread assignment, same
+// results).
+template <int KR>
+__global__ __launch_bounds__(1024) void add_rmsnorm_regs_kernel(float* x, const float* delta, const float* w,
+                                                                float* out, int n, float eps) {
+    __shared__ float red[16];
+    x += (size_t)blockIdx.x * n;
+    delta += (size_t)blockIdx.x * n;
+    out += (size_t)blockIdx.x * n;
+    float v[KR], ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+        const int i = threadIdx.x + 1024 * k;
+        if (i < n) {
+            v[k] = x[i] + delta[i];
+            x[i] = v[k];
+            ss += v[k] * v[k];
+        }
+    }
+    const float total = block_sum(ss, red);
+    const float scale = 1.f / sqrtf(total / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+        const int i = threadIdx.x + 1024 * k;
+        if (i < n) out[i] = v[k] * (scale * w[i]);
+    }
+}
+
 __global__ void add_kernel(float* x, const float* y, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) x[i] += y[i];
@@ -157,7 +186,12 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int n
 hipError_t launch_add_rmsnorm_rows(float* x, const float* delta, const float* w, float* out, int n, int rows, float eps,
                                   hipStream_t stream) {
     if (rows < 1) return hipErrorInvalidValue;
-    launch_kernel(add_rmsnorm_kernel, dim3(rows), dim3(1024), 0, stream, x, delta, w, out, n, eps);
+    if (n <= 1024 * 4)
+        launch_kernel(add_rmsnorm_regs_kernel<4>, dim3(rows), dim3(1024), 0, stream, x, delta, w, out, n, eps);
+    else if (n <= 1024 * 8)
+        launch_kernel(add_rmsnorm_regs_kernel<8>, dim3(rows), dim3(1024), 0, stream, x, delta, w, out, n, eps);
+    else
+        launch_kernel(add_rmsnorm_kernel, dim3(rows), dim3(1024), 0, stream, x, delta, w, out, n, eps);
     return hipGetLastError();
 }
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t stream) {
