@@ -381,8 +381,6 @@ def main():
     ap.add_argument("--trace-steps", type=int, default=3)
     ap.add_argument("--no-graph", action="store_true",
                     help="launch every kernel from the host instead of replaying the step graph (for profilers)")
-    ap.add_argument("--step-program", action="store_true",
-                    help="replay each step as the persistent step kernel instead of the per-op graph")
     ap.add_argument("--copy-probe", type=int, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (counter calibration) and exit")
     ap.add_argument("--attention-probe", type=int, metavar="KV_LEN",
@@ -417,8 +415,7 @@ def main():
     import emprise_amd as ea
     path = model_file(args.model, seed=0)
     t = time.time()
-    model = ea.Model(path, context=args.context, fast_q8=args.fast_q8, graph=not args.no_graph,
-                     step_program=args.step_program)
+    model = ea.Model(path, context=args.context, fast_q8=args.fast_q8, graph=not args.no_graph)
     info = model.info
     log(f"loaded {path.name}: {info.weight_bytes / 1e9:.3f} GB on device in {time.time() - t:.1f}s "
         f"({model.backend_name}); {info.token_weight_bytes / 1e9:.4f} GB streamed per token")
@@ -436,10 +433,9 @@ def main():
         raise RuntimeError(f"generation stopped early ({len(tokens)} of {count} tokens)")
     decode_s = arrivals[-1] - arrivals[0]
     value = args.steps / decode_s
-    program = model.step_program == 1
     log(f"prefill {args.prompt} tokens in {arrivals[0]:.3f}s, {args.steps} decode steps in {decode_s:.4f}s "
         f"-> {value:.1f} tok/s (host wall {wall:.3f}s; "
-        f"{'persistent step kernel' if program else 'per-op launches, no graph' if args.no_graph else 'per-op step graph'})")
+        f"{'per-op launches, no graph' if args.no_graph else 'per-op step graph'})")
 
     # per-kernel timing of eager steps right after the timed region (same positions range)
     trace = []
@@ -491,7 +487,7 @@ def main():
         "config": {"workload": workload + (" (--fast-q8)" if args.fast_q8 else ""), "prompt_tokens": args.prompt,
                    "generated_tokens": count, "context": args.context, "hidden": info.hidden, "layers": info.layers,
                    "vocab": info.vocab, "token_weight_bytes": info.token_weight_bytes,
-                   "step": "persistent step kernel" if program else "per-op graph",
+                   "step": "per-op launches" if args.no_graph else "per-op graph",
                    "parallelism": "single GPU"},
         "hbm_roofline_fraction": round(e2e_gbs / HBM_PEAK_GBS, 4),
         "roofline": roofline,

@@ -110,7 +110,6 @@ def hip_lib() -> ctypes.CDLL:
         "emprise_hip_lm_head": (st, [vp, vp, u64, u64, u64]),
         "emprise_hip_graph_begin": (st, [vp]),
         "emprise_hip_graph_end": (st, [vp, P(u64)]),
-        "emprise_hip_set_step_program": (st, [vp, ctypes.c_int]),
         "emprise_hip_graph_launch": (st, [vp, u64]),
         "emprise_hip_graph_destroy": (st, [vp, u64]),
         "emprise_hip_event_record": (st, [vp, i32]),
@@ -345,11 +344,6 @@ class HipBackend:
     def sync(self):
         self._check(self.lib.emprise_hip_sync(self.h))
 
-    def set_step_program(self, enable: bool):
-        """Record graph_begin..graph_end as one persistent step kernel (see
-        emprise_hip_set_step_program); graph_end raises on sequences it cannot express."""
-        self._check(self.lib.emprise_hip_set_step_program(self.h, int(enable)))
-
     def graph_begin(self):
         self._check(self.lib.emprise_hip_graph_begin(self.h))
 
@@ -387,8 +381,15 @@ def gpu_available() -> bool:
 class ModelOptions(ctypes.Structure):
     _fields_ = [("path", ctypes.c_char_p), ("context", ctypes.c_size_t), ("device", ctypes.c_int),
                 ("weight_vram_budget", ctypes.c_uint64), ("quantize_activations", ctypes.c_int),
-                ("fused", ctypes.c_int), ("graph", ctypes.c_int), ("batch_prefill", ctypes.c_int),
-                ("step_program", ctypes.c_int)]
+                ("fused", ctypes.c_int), ("graph", ctypes.c_int), ("batch_prefill", ctypes.c_int)]
+
+
+class ModelProfile(ctypes.Structure):
+    _fields_ = [("matrix_seconds", ctypes.c_double), ("non_matrix_seconds", ctypes.c_double),
+                ("norm_seconds", ctypes.c_double), ("attention_seconds", ctypes.c_double),
+                ("recurrent_seconds", ctypes.c_double), ("matrix_calls", ctypes.c_uint64),
+                ("evaluated_tokens", ctypes.c_uint64), ("decode_steps", ctypes.c_uint64),
+                ("traced_steps", ctypes.c_uint64)]
 
 
 class ModelInfo(ctypes.Structure):
@@ -450,8 +451,8 @@ def host_lib() -> ctypes.CDLL:
     lib.emprise_model_backend_name.argtypes = [vp]
     lib.emprise_model_get_info.restype = ctypes.c_int
     lib.emprise_model_get_info.argtypes = [vp, P(ModelInfo)]
-    lib.emprise_model_step_program.restype = ctypes.c_int
-    lib.emprise_model_step_program.argtypes = [vp]
+    lib.emprise_model_get_profile.restype = ctypes.c_int
+    lib.emprise_model_get_profile.argtypes = [vp, P(ModelProfile)]
     lib.emprise_model_reset.restype = ctypes.c_int
     lib.emprise_model_reset.argtypes = [vp]
     lib.emprise_model_evaluate.restype = ctypes.c_int
@@ -588,15 +589,13 @@ class Model:
     """The C++ host's qwen35 model on the MI355X (Model::Model / evaluate / generate)."""
 
     def __init__(self, path, context: int = 4096, device: int = 0, vram_budget: int = 0, fast_q8: bool = False,
-                 fused: bool = True, graph: bool = True, batch_prefill: int = 0, step_program: bool = False):
+                 fused: bool = True, graph: bool = True, batch_prefill: int = 0):
         """batch_prefill: prompts with at least this many tokens before the last prefill
-        in batches (GEMM projections); 0 = the library default (64), -1 = never.
-        step_program: replay each decode step as one persistent kernel where the shapes allow
-        (slower than the per-op graph on the MI355X; kept as an option)."""
+        in batches (GEMM projections); 0 = the library default (64), -1 = never."""
         lib = host_lib()
         self._path = str(path).encode()
         o = ModelOptions(self._path, context, device, vram_budget, int(fast_q8), int(fused), int(graph),
-                         int(batch_prefill), int(step_program))
+                         int(batch_prefill))
         m = ctypes.c_void_p()
         _host_check(lib.emprise_model_open(ctypes.byref(o), ctypes.byref(m)))
         self.m = m
@@ -606,11 +605,6 @@ class Model:
     @property
     def backend_name(self) -> str:
         return host_lib().emprise_model_backend_name(self.m).decode()
-
-    @property
-    def step_program(self) -> int:
-        """1: decode steps run as a persistent step kernel; 0: per-op graphs; -1: not yet known."""
-        return host_lib().emprise_model_step_program(self.m)
 
     def close(self):
         if getattr(self, "m", None):
@@ -683,6 +677,12 @@ class Model:
 
     def reset_mtp(self):
         _host_check(host_lib().emprise_model_reset_mtp(self.m))
+
+    def profile(self) -> dict:
+        """Model::profile (emprise_model_get_profile)."""
+        p = ModelProfile()
+        _host_check(host_lib().emprise_model_get_profile(self.m, ctypes.byref(p)))
+        return {k: getattr(p, k) for k, _ in ModelProfile._fields_}
 
     def trace_step(self, token: int):
         """One eager step with per-launch HIP event timing: [(kernel, bytes, ms), ...]."""

@@ -176,7 +176,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     lds_barrier();
     // NEOX RoPE over the first `rotary` dims (model.cpp:121-127); one thread per pair,
     // the angles' cos and sin from the backend's table (rope_table_kernel), which the
-    // step program and the batched prefill read as well
+    // batched prefill reads as well
     for (int idx = threadIdx.x; idx < (group + 1) * half; idx += blockDim.x) {
         const int g = idx / half, i = idx % half;
         float* row = g < group ? qs[g] : knew;
@@ -604,9 +604,8 @@ hipError_t launch_rope_table(float2* table, int context, int rotary, float base,
 }
 
 size_t attention_partial_floats(int heads, int kv_heads, int head_dim, int context) {
-    // partials of the per-op kernel (kAttnSplit ranges) or of the step program's chunks
-    const int chunks = std::max(kAttnSplit, (context + kAttnChunk - 1) / kAttnChunk);
-    return (size_t)kv_heads * chunks * (heads / kv_heads) * (head_dim + 2);
+    (void)context;  // the grid has kAttnSplit ranges at every context length
+    return (size_t)kv_heads * kAttnSplit * (heads / kv_heads) * (head_dim + 2);
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {

@@ -4,7 +4,6 @@
 #include "common.hpp"
 #include "kernels.hpp"
 #include "layout.hpp"
-#include "step.hpp"
 
 #include <algorithm>
 #include <cstdarg>
@@ -84,35 +83,6 @@ void parallel_copy(uint8_t* dst, const uint8_t* src, uint64_t n) {
     });
 }
 
-// ---- step-program recording (emprise_hip_set_step_program) ----------------------------
-
-// An output range of a recorded phase inside a host buffer: `sel` names the phase's
-// output operand (0..kMaxSeg-1 matvec segment y, then the StepSel values).
-enum StepSel : int { kSelXOut = kMaxSeg, kSelGdnOut, kSelPartial, kSelAttnOut };
-struct StepWrite {
-    size_t off, len;  // floats from the start of the host allocation
-    int phase;        // the writing phase
-    int tag_phase;    // the phase index its tags carry
-    int sel, consumers;
-    uintptr_t host;
-};
-// Tagged mirror of one host allocation: 8-byte {value, tag} slots, one per float.
-struct StepMirror {
-    size_t bytes = 0;
-    void* dev = nullptr;
-    std::vector<StepWrite> writes;
-};
-// The embedding row a recorded embed call left in a host buffer, decoded lazily by the
-// matvec phases that read it.
-struct StepEmbed {
-    uintptr_t host;
-    size_t floats;
-    const uint8_t* w;
-    uint32_t type;
-    int rows;
-    const int* token;
-};
-
 }  // namespace
 
 // Scratch of emprise_hip_delta_net_noalloc: the conv'd channels of one GDN step, in a
@@ -158,23 +128,6 @@ struct emprise_hip {
         uint64_t bytes;
         hipEvent_t a, b;
     };
-    // step programs
-    bool step_mode = false, recording = false, step_launched = false;
-    std::string rec_error;
-    std::vector<StepPhase> rec;
-    std::map<uintptr_t, StepMirror> mirrors;
-    std::vector<StepEmbed> embeds;
-    struct Finish {
-        unsigned long long* key = nullptr;
-        int* index = nullptr;
-        int* state = nullptr;
-        const int* prompt = nullptr;
-        int* history = nullptr;
-        const int* next = nullptr;
-    } fin;
-    uint32_t* step_epoch = nullptr;
-    uint32_t* step_err = nullptr;
-    std::unordered_map<uint64_t, StepPhase*> program_of;  // graph id -> device program
     bool tracing = false;
     std::vector<TraceRec> trace;
     std::vector<hipEvent_t> trace_pool;
@@ -218,13 +171,7 @@ emprise_status launched(hipError_t e) {
 
 // Launches through `launch`; while tracing, the launch's kernels carry a start/stop
 // event pair on their dispatch packets and the op's algorithmic bytes are recorded.
-emprise_status rec_unsupported(emprise_hip* h, const char* what) {
-    if (h->rec_error.empty()) h->rec_error = what;
-    return EMPRISE_OK;
-}
-
 template <class F> emprise_status traced(emprise_hip* h, const char* kernel, uint64_t bytes, F launch) {
-    if (h->recording) return rec_unsupported(h, kernel);
     if (!h->tracing) return launched(launch());
     hipEvent_t a = h->trace_event(), b = h->trace_event();
     if (!a || !b) return fail(EMPRISE_EDEVICE, "trace event");
@@ -272,14 +219,9 @@ struct HeadGate {
     float eps;
 };
 
-emprise_status rec_matvec(emprise_hip* h, const Proj* p, int n, int mode, const emprise_hip_input* in,
-                          const float* x_plain, const float* conv_w, float* conv_state, int conv_width,
-                          unsigned long long* argmax_key, const HeadGate* hg);
-
 emprise_status run_matvec(emprise_hip* h, const Proj* p, int n, int mode, const emprise_hip_input* in,
                           const float* x_plain, const float* conv_w, float* conv_state, int conv_width,
                           unsigned long long* argmax_key, const HeadGate* hg = nullptr) {
-    if (h->recording) return rec_matvec(h, p, n, mode, in, x_plain, conv_w, conv_state, conv_width, argmax_key, hg);
     if (n < 1 || n > kMaxSeg) return fail(EMPRISE_EINVAL, "between 1 and %d projections per call", kMaxSeg);
     const uint64_t cols = p[0].w->cols;
     for (int i = 0; i < n; ++i)
@@ -361,207 +303,6 @@ emprise_status check_weights(emprise_hip* h, int n, const emprise_weight* ids, c
     return EMPRISE_OK;
 }
 
-// ---- step-program recording ---------------------------------------------------------
-
-// The tagged mirror of the host allocation holding p (created zeroed on first use; a
-// zero slot never carries a live tag, since tags start at epoch 1).
-emprise_status mirror_of(emprise_hip* h, const void* p, StepMirror** out, size_t* off) {
-    void* base = nullptr;
-    size_t size = 0;
-    HIP_TRY(hipMemGetAddressRange(&base, &size, const_cast<void*>(p)));
-    const uintptr_t key = reinterpret_cast<uintptr_t>(base), at = reinterpret_cast<uintptr_t>(p);
-    if ((at - key) % 4) return fail(EMPRISE_EINVAL, "step program operand not float-aligned");
-    StepMirror& m = h->mirrors[key];
-    if (m.bytes != size) {
-        if (m.dev) HIP_TRY(hipFree(m.dev));
-        m.dev = nullptr;
-        m.bytes = 0;
-        HIP_TRY(hipMalloc(&m.dev, 2 * size));
-        HIP_TRY(hipMemset(m.dev, 0, 2 * size));
-        m.bytes = size;
-    }
-    *out = &m;
-    *off = (at - key) / 4;
-    return EMPRISE_OK;
-}
-
-// Registers that phase h->rec.size() writes n floats at host address p, tagged with
-// phase `tag_phase`.
-emprise_status rec_write(emprise_hip* h, void* p, size_t n, int sel, int tag_phase, StepOut* out) {
-    StepMirror* m;
-    size_t off;
-    TRY(mirror_of(h, p, &m, &off));
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    for (size_t i = 0; i < h->embeds.size();)
-        if (h->embeds[i].host < a + n * 4 && a < h->embeds[i].host + h->embeds[i].floats * 4)
-            h->embeds.erase(h->embeds.begin() + (long)i);
-        else
-            ++i;
-    m->writes.push_back({off, n, (int)h->rec.size(), tag_phase, sel, 0, a});
-    *out = StepOut{static_cast<char*>(m->dev) + off * 8, 1};
-    return EMPRISE_OK;
-}
-
-// Resolves a read of n floats at host address p: the tagged slots of the latest phase
-// that wrote them in this program, or the plain buffer if none did.
-emprise_status rec_read(emprise_hip* h, const void* p, size_t n, StepIn* out) {
-    *out = StepIn{p, -1};
-    void* base = nullptr;
-    size_t size = 0;
-    HIP_TRY(hipMemGetAddressRange(&base, &size, const_cast<void*>(p)));
-    auto it = h->mirrors.find(reinterpret_cast<uintptr_t>(base));
-    if (it == h->mirrors.end() || it->second.bytes != size) return EMPRISE_OK;
-    StepMirror& m = it->second;
-    const size_t off = (reinterpret_cast<uintptr_t>(p) - reinterpret_cast<uintptr_t>(base)) / 4;
-    int last = -1;
-    for (const StepWrite& w : m.writes)
-        if (w.off < off + n && off < w.off + w.len) last = std::max(last, w.tag_phase);
-    if (last < 0) return EMPRISE_OK;
-    // the latest producing call must cover the whole range (one tag per read)
-    std::vector<std::pair<size_t, size_t>> spans;
-    for (StepWrite& w : m.writes)
-        if (w.tag_phase == last && w.off < off + n && off < w.off + w.len) {
-            spans.push_back({w.off, w.off + w.len});
-            ++w.consumers;
-        }
-    std::sort(spans.begin(), spans.end());
-    size_t covered = off;
-    for (auto& sp : spans)
-        if (sp.first <= covered) covered = std::max(covered, sp.second);
-    if (covered < off + n) return rec_unsupported(h, "read spanning several producers");
-    *out = StepIn{static_cast<char*>(m.dev) + off * 8, last};
-    return EMPRISE_OK;
-}
-
-// Matvec phases of a run_matvec call (same grouping into equal-type runs).
-emprise_status rec_matvec(emprise_hip* h, const Proj* p, int n, int mode, const emprise_hip_input* in,
-                          const float* x_plain, const float* conv_w, float* conv_state, int conv_width,
-                          unsigned long long* argmax_key, const HeadGate* hg) {
-    if (h->q8) return rec_unsupported(h, "Q8 activations");
-    if (n < 1 || n > kMaxSeg) return fail(EMPRISE_EINVAL, "between 1 and %d projections per call", kMaxSeg);
-    const uint64_t cols = p[0].w->cols;
-    for (int i = 0; i < n; ++i) {
-        if (p[i].w->cols != cols) return fail(EMPRISE_EINVAL, "projections sharing an input need equal columns");
-        if (p[i].w->type != kQ6K && p[i].w->type != kQ4K) return rec_unsupported(h, "non-k-quant projection");
-    }
-    if (cols % kChunkCols || cols > (uint64_t)kStepMaxCols) return rec_unsupported(h, "projection width");
-    const bool transform = (in && (in->delta || in->x_out || in->norm)) || hg || conv_w || mode == kMvSwiglu;
-    if (cols > 4 * 2 * kStepWaves * 64 && transform) return rec_unsupported(h, "wide input with a transform");
-    if (hg && (hg->head_dim < 4 || hg->head_dim > 256 || hg->head_dim % 4 ||
-               ((hg->head_dim / 4) & (hg->head_dim / 4 - 1)) || cols % hg->head_dim))
-        return rec_unsupported(h, "per-head gate shape");
-    if (conv_w && conv_width * kMvStreamRows > 64) return rec_unsupported(h, "conv width");
-    for (int i = 0; i < n; ++i)
-        if (p[i].silu && !conv_w) return rec_unsupported(h, "SiLU'd rows without the conv epilogue");
-    // the input operands are resolved before any output of this call is registered
-    StepIn x{}, delta{nullptr, -1}, gate{nullptr, -1};
-    const StepEmbed* emb = nullptr;
-    const void* xp = in ? reinterpret_cast<const void*>(in->x) : x_plain;
-    for (const StepEmbed& e : h->embeds)
-        if (e.host == reinterpret_cast<uintptr_t>(xp) && e.floats == cols) emb = &e;
-    if (!emb) TRY(rec_read(h, xp, cols, &x));
-    if (in && in->delta) TRY(rec_read(h, reinterpret_cast<const void*>(in->delta), cols, &delta));
-    if (hg) TRY(rec_read(h, hg->gate, cols, &gate));
-    const float* norm = nullptr;
-    if (in && in->norm) {
-        const Weight* nw = h->weight(in->norm);
-        if (!nw || nw->type != kF32 || nw->rows * nw->cols != cols)
-            return fail(EMPRISE_EINVAL, "norm weight must be F32 with %llu elements", (unsigned long long)cols);
-        norm = reinterpret_cast<const float*>(nw->dev);
-    }
-    bool first = true;
-    const int call_phase = (int)h->rec.size();  // every run's outputs carry this phase's tag
-    for (int i = 0; i < n;) {
-        int j = i + 1;
-        if (mode != kMvSwiglu)
-            while (j < n && p[j].w->type == p[i].w->type) ++j;
-        else
-            j = n;
-        if (mode == kMvSwiglu && p[0].w->type != p[1].w->type) return rec_unsupported(h, "mixed gate/up types");
-        StepPhase ph{};
-        ph.kind = kStepMatvec;
-        ph.tag_phase = call_phase;
-        StepMatvec& m = ph.mv;
-        m.type = p[i].w->type;
-        m.mode = mode;
-        m.cols = (int)cols;
-        m.nseg = j - i;
-        uint64_t total_rows = 0;
-        for (int s2 = 0; s2 < m.nseg; ++s2)
-            if (!(mode == kMvSwiglu && s2 == 1)) total_rows += p[i + s2].w->rows;
-        const int R = matvec_rows_per_group(m.type, cols, mode, total_rows);
-        m.rows_per_group = R;
-        int g = 0;
-        for (int s2 = 0; s2 < m.nseg; ++s2) {
-            const Weight* w = p[i + s2].w;
-            m.seg[s2].w = w->dev;
-            m.seg[s2].rows = (int)w->rows;
-            if (p[i + s2].silu) m.silu_mask |= 1 << s2;
-            m.seg[s2].g0 = g;
-            if (mode == kMvSwiglu && s2 == 1) m.seg[s2].g0 = 0x7fffffff;
-            else g += (int)((w->rows + R - 1) / R);
-            if (p[i + s2].y) TRY(rec_write(h, p[i + s2].y, w->rows, s2, call_phase, &m.seg[s2].y));
-        }
-        m.groups = g;
-        m.x = x;
-        m.delta = delta;
-        m.gate = gate;
-        m.norm = hg ? hg->norm : norm;
-        m.eps = hg ? hg->eps : (in ? in->eps : 0.f);
-        m.head_dim = hg ? hg->head_dim : 0;
-        if (emb) {
-            m.emb = emb->w;
-            m.emb_type = emb->type;
-            m.emb_rows = emb->rows;
-            m.token = emb->token;
-        }
-        if (first && in && in->x_out)
-            TRY(rec_write(h, reinterpret_cast<void*>(in->x_out), cols, kSelXOut, call_phase, &m.x_out));
-        if (first && conv_w) {
-            m.conv_w = conv_w;
-            m.conv_state = conv_state;
-            m.conv_width = conv_width;
-        }
-        m.argmax = argmax_key;
-        h->rec.push_back(ph);
-        first = false;
-        i = j;
-    }
-    return EMPRISE_OK;
-}
-
-StepOut* step_out_of(StepPhase& ph, int sel) {
-    if (sel < kMaxSeg) return &ph.mv.seg[sel].y;
-    switch (sel) {
-    case kSelXOut: return &ph.mv.x_out;
-    case kSelGdnOut: return &ph.gdn.out;
-    case kSelPartial: return &ph.attn.partial;
-    default: return &ph.attn.out;
-    }
-}
-
-void rec_reset(emprise_hip* h) {
-    h->rec.clear();
-    h->rec_error.clear();
-    h->embeds.clear();
-    for (auto& kv : h->mirrors) kv.second.writes.clear();
-    h->fin = {};
-}
-
-// Checks a program graph's error word after the stream has drained.
-emprise_status check_step(emprise_hip* h) {
-    if (!h->step_launched) return EMPRISE_OK;
-    h->step_launched = false;
-    uint32_t e = 0;
-    HIP_TRY(hipMemcpy(&e, h->step_err, sizeof e, hipMemcpyDeviceToHost));
-    if (e) {
-        const uint32_t zero = 0;
-        HIP_TRY(hipMemcpy(h->step_err, &zero, sizeof zero, hipMemcpyHostToDevice));
-        return fail(EMPRISE_EDEVICE, "decode-step program: a phase waited past its deadline");
-    }
-    return EMPRISE_OK;
-}
-
 }  // namespace
 
 extern "C" {
@@ -609,10 +350,6 @@ void emprise_hip_destroy(emprise_hip* h) {
     (void)hipSetDevice(h->device);
     (void)hipStreamSynchronize(h->stream);
     for (auto& kv : h->graphs) (void)hipGraphExecDestroy(kv.second);
-    for (auto& kv : h->program_of) (void)hipFree(kv.second);
-    for (auto& kv : h->mirrors) (void)hipFree(kv.second.dev);
-    if (h->step_epoch) (void)hipFree(h->step_epoch);
-    if (h->step_err) (void)hipFree(h->step_err);
     for (auto& kv : h->weights) (void)hipFree(kv.second.dev);
     for (auto& kv : h->scratch) (void)hipFree(kv.second.ptr);
     for (int k = 0; k < 2; ++k) {
@@ -659,7 +396,7 @@ emprise_status emprise_hip_download(emprise_hip* h, void* dst, emprise_dev src, 
     if (h->capturing) return fail(EMPRISE_ESTATE, "download during graph capture");
     HIP_TRY(hipMemcpyAsync(dst, reinterpret_cast<const void*>(src), bytes, hipMemcpyDeviceToHost, h->stream));
     HIP_TRY(hipStreamSynchronize(h->stream));
-    return check_step(h);
+    return EMPRISE_OK;
 }
 
 emprise_status emprise_hip_fill(emprise_hip* h, emprise_dev dst, float value, size_t n) {
@@ -768,7 +505,6 @@ emprise_status emprise_hip_dequantize_rows(emprise_hip* h, emprise_weight id, ui
     if (!w || !out) return fail(EMPRISE_EINVAL, "bad weight or output");
     if (row0 > w->rows || n > w->rows - row0) return fail(EMPRISE_EINVAL, "rows out of range");
     if (!n) return EMPRISE_OK;
-    if (h->recording) return rec_unsupported(h, "dequantize_rows");
     return launched(launch_dequant_rows(w->dev, w->type, (int)w->cols, row0, n, reinterpret_cast<float*>(out), h->stream));
 }
 
@@ -1099,17 +835,6 @@ emprise_status emprise_hip_swiglu(emprise_hip* h, emprise_dev gate, emprise_dev 
 emprise_status emprise_hip_embed(emprise_hip* h, emprise_weight embedding, emprise_dev token, emprise_dev out) {
     const Weight* w = h ? h->weight(embedding) : nullptr;
     if (!w || !token || !out) return fail(EMPRISE_EINVAL, "bad arguments");
-    if (h->recording) {
-        // decoded by the matvec phases that read the row (rec_matvec)
-        const uintptr_t a = static_cast<uintptr_t>(out);
-        for (size_t i = 0; i < h->embeds.size();)
-            if (h->embeds[i].host < a + w->cols * 4 && a < h->embeds[i].host + h->embeds[i].floats * 4)
-                h->embeds.erase(h->embeds.begin() + (long)i);
-            else
-                ++i;
-        h->embeds.push_back({a, w->cols, w->dev, w->type, (int)w->rows, reinterpret_cast<const int*>(token)});
-        return EMPRISE_OK;
-    }
     return traced(h, "embed", w->bytes / w->rows + w->cols * 4, [&] { return launch_embed(w->dev, w->type, (int)w->cols, (int)w->rows, reinterpret_cast<const int*>(token),
                                  reinterpret_cast<float*>(out), h->stream); });
 }
@@ -1177,7 +902,6 @@ emprise_status emprise_hip_delta_net_noalloc(emprise_hip* h, const emprise_hip_d
     if (!p->qkv || !p->gate || !p->alpha || !p->beta || !p->conv_state || !p->rec_state || !p->out)
         return fail(EMPRISE_EINVAL, "null buffer");
     if (p->rec_state % 16) return fail(EMPRISE_EINVAL, "rec_state must be 16-byte aligned");
-    if (h->recording) return fail(EMPRISE_ESTATE, "delta_net_noalloc is not recorded into step programs");
     // the conv kernel writes all ch channels of the scratch before the state update reads
     // them, so nothing carried over from an earlier call is read
     float* conv_out = h->noalloc_scratch;
@@ -1218,7 +942,6 @@ emprise_status emprise_hip_delta_net_batch(emprise_hip* h, const emprise_hip_del
     if (count < 1 || count > (1 << 19) || stride < (uint64_t)ch || out_stride < (uint64_t)vd)
         return fail(EMPRISE_EINVAL, "delta_net_batch: count %d, stride %llu, out_stride %llu", count,
                     (unsigned long long)stride, (unsigned long long)out_stride);
-    if (h->recording) return rec_unsupported(h, "batched delta_net");
     void *conv_out, *o, *qk, *gates;
     TRY(h->get_scratch("gdn_conv_batch", (size_t)count * ch * sizeof(float), &conv_out));
     TRY(h->get_scratch("gdn_o_batch", (size_t)count * vd * sizeof(float), &o));
@@ -1303,27 +1026,6 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
     g.state = reinterpret_cast<float*>(p->rec_state);
     g.out = dn;
     Proj po{w[4], reinterpret_cast<float*>(y)};
-    if (h->recording) {
-        if (!split) return rec_unsupported(h, "recurrent output width");
-        StepPhase ph{};
-        ph.kind = kStepGdn;
-        StepGdn& sg = ph.gdn;
-        sg.key_heads = p->key_heads;
-        sg.value_heads = p->value_heads;
-        sg.state_dim = p->state_dim;
-        sg.eps = p->eps;
-        TRY(rec_read(h, qkv, (size_t)ch, &sg.qkv));
-        TRY(rec_read(h, alpha, (size_t)p->value_heads, &sg.alpha));
-        TRY(rec_read(h, beta, (size_t)p->value_heads, &sg.beta));
-        sg.ssm_a = g.ssm_a;
-        sg.dt = g.dt;
-        sg.state = g.state;
-        ph.tag_phase = (int)h->rec.size();
-        TRY(rec_write(h, dn, (size_t)vd, kSelGdnOut, ph.tag_phase, &sg.out));
-        h->rec.push_back(ph);
-        const HeadGate hg{gate, g.norm, p->state_dim, p->eps};
-        return run_matvec(h, &po, 1, kMvPlain, nullptr, dn, nullptr, nullptr, 0, nullptr, &hg);
-    }
     if (split) {
         TRY(traced(h, "gdn_step", gdn_bytes(g) - (uint64_t)vd * 4, [&] { return launch_gdn_rows(g, h->stream); }));
         const HeadGate hg{gate, g.norm, p->state_dim, p->eps};
@@ -1335,7 +1037,7 @@ emprise_status emprise_hip_recurrent(emprise_hip* h, const emprise_hip_recurrent
 
 namespace {
 // The RoPE table (cos, sin of every position's angles) of this (context, rotary, base),
-// shared by the decode, step-program and prefill attention so that they rotate with the
+// shared by the decode and prefill attention so that they rotate with the
 // same values; filled by the first eager call (not while a graph is being captured).
 emprise_status rope_table(emprise_hip* h, const emprise_hip_attention_params* p, const float2** out) {
     uint32_t bits;
@@ -1369,7 +1071,6 @@ emprise_status emprise_hip_attention_batch(emprise_hip* h, const emprise_hip_att
         out_stride < (uint64_t)p->heads * p->head_dim)
         return fail(EMPRISE_EINVAL, "attention_batch: positions %d..%d of a %d-position context, stride %llu",
                     first_position, first_position + count - 1, p->context, (unsigned long long)stride);
-    if (h->recording) return rec_unsupported(h, "batched attention");
     AttnBatchArgs a{};
     TRY(rope_table(h, p, &a.rope));
     a.heads = p->heads;
@@ -1434,44 +1135,6 @@ emprise_status emprise_hip_attention(emprise_hip* h, const emprise_hip_attention
     a.out = reinterpret_cast<float*>(out);
     a.partial = static_cast<float*>(partial);
     TRY(rope_table(h, p, &a.rope));
-    if (h->recording) {
-        if (p->rope_position) return rec_unsupported(h, "a rotary position apart from the cache row");
-        const int chunks = (p->context + kAttnChunk - 1) / kAttnChunk;
-        if ((p->head_dim != 128 && p->head_dim != 256) || chunks > 1024)
-            return rec_unsupported(h, "attention shape");
-        const size_t qkv_n = (size_t)p->heads * p->head_dim * 2 + 2 * (size_t)p->kv_heads * p->head_dim;
-        const size_t part_n = attention_partial_floats(p->heads, p->kv_heads, p->head_dim, p->context);
-        StepPhase ph{};
-        ph.kind = kStepAttention;
-        StepAttention& sa = ph.attn;
-        sa.heads = a.heads;
-        sa.kv_heads = a.kv_heads;
-        sa.head_dim = a.head_dim;
-        sa.rotary = a.rotary;
-        sa.context = a.context;
-        sa.eps = a.eps;
-        sa.rope_base = a.rope_base;
-        sa.rope = a.rope;
-        sa.q_norm = a.q_norm;
-        sa.k_norm = a.k_norm;
-        sa.keys = a.keys;
-        sa.values = a.values;
-        sa.position = a.position;
-        TRY(rec_read(h, a.qkv, qkv_n, &sa.qkv));
-        sa.partial_in = StepIn{nullptr, -1};
-        ph.tag_phase = (int)h->rec.size();
-        TRY(rec_write(h, a.partial, part_n, kSelPartial, ph.tag_phase, &sa.partial));
-        h->rec.push_back(ph);
-        StepPhase pc = ph;
-        pc.kind = kStepCombine;
-        pc.attn.partial = StepOut{nullptr, 0};
-        TRY(rec_read(h, a.qkv, qkv_n, &pc.attn.qkv));
-        TRY(rec_read(h, a.partial, part_n, &pc.attn.partial_in));
-        pc.tag_phase = (int)h->rec.size();
-        TRY(rec_write(h, a.out, (size_t)p->heads * p->head_dim, kSelAttnOut, pc.tag_phase, &pc.attn.out));
-        h->rec.push_back(pc);
-        return EMPRISE_OK;
-    }
     return traced(h, "attention", 0, [&] { return launch_attention(a, h->stream); });
 }
 
@@ -1484,19 +1147,12 @@ emprise_status emprise_hip_sync(emprise_hip* h) {
     if (!h) return fail(EMPRISE_EINVAL, "null backend");
     if (h->capturing) return fail(EMPRISE_ESTATE, "sync during graph capture");
     HIP_TRY(hipStreamSynchronize(h->stream));
-    return check_step(h);
+    return EMPRISE_OK;
 }
 
 emprise_status emprise_hip_advance(emprise_hip* h, emprise_dev state, emprise_dev prompt, emprise_dev history,
                                    emprise_dev next) {
     if (!h || !state) return fail(EMPRISE_EINVAL, "null argument");
-    if (h->recording) {
-        h->fin.state = reinterpret_cast<int*>(state);
-        h->fin.prompt = reinterpret_cast<const int*>(prompt);
-        h->fin.history = reinterpret_cast<int*>(history);
-        h->fin.next = reinterpret_cast<const int*>(next);
-        return EMPRISE_OK;
-    }
     return traced(h, "advance", 16, [&] { return launch_advance(reinterpret_cast<int*>(state), reinterpret_cast<const int*>(prompt),
                                    reinterpret_cast<int*>(history), reinterpret_cast<const int*>(next), h->stream); });
 }
@@ -1511,96 +1167,20 @@ emprise_status emprise_hip_lm_head(emprise_hip* h, const emprise_hip_input* in, 
     TRY(h->get_scratch("argmax_key", sizeof(unsigned long long), &key, true));
     Proj p{wt, reinterpret_cast<float*>(logits)};
     TRY(run_matvec(h, &p, 1, kMvArgmax, in, nullptr, nullptr, nullptr, 0, static_cast<unsigned long long*>(key)));
-    if (h->recording) {
-        h->fin.key = static_cast<unsigned long long*>(key);
-        h->fin.index = reinterpret_cast<int*>(index);
-        return EMPRISE_OK;
-    }
     return traced(h, "argmax_finish", 16, [&] { return launch_argmax_finish(static_cast<unsigned long long*>(key), reinterpret_cast<int*>(index), h->stream); });
-}
-
-emprise_status emprise_hip_set_step_program(emprise_hip* h, int enable) {
-    if (!h) return fail(EMPRISE_EINVAL, "null backend");
-    if (h->capturing) return fail(EMPRISE_ESTATE, "mode change during capture");
-    h->step_mode = enable != 0;
-    return EMPRISE_OK;
 }
 
 emprise_status emprise_hip_graph_begin(emprise_hip* h) {
     if (!h) return fail(EMPRISE_EINVAL, "null backend");
     if (h->capturing) return fail(EMPRISE_ESTATE, "already capturing");
-    if (h->step_mode) {
-        rec_reset(h);
-        h->recording = true;
-        h->capturing = true;
-        return EMPRISE_OK;
-    }
     HIP_TRY(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
     h->capturing = true;
     return EMPRISE_OK;
 }
 
-namespace {
-// Finishes a recording: outputs no later phase reads become plain stores into the
-// caller's buffers, the program goes to device memory, and the step kernel + finish
-// kernel are captured as the returned graph.
-emprise_status finish_program(emprise_hip* h, emprise_graph* out) {
-    if (!h->rec_error.empty())
-        return fail(EMPRISE_EUNSUPPORTED, "step program: unsupported call or shape (%s)", h->rec_error.c_str());
-    if (h->rec.empty() || h->rec.size() > (size_t)kStepMaxPhases)
-        return fail(EMPRISE_EUNSUPPORTED, "step program: %zu phases", h->rec.size());
-    for (auto& kv : h->mirrors)
-        for (const StepWrite& w : kv.second.writes)
-            if (!w.consumers) *step_out_of(h->rec[(size_t)w.phase], w.sel) = StepOut{reinterpret_cast<void*>(w.host), 0};
-    size_t lds = 0;
-    for (const StepPhase& ph : h->rec) lds = std::max(lds, step_phase_lds(ph));
-    const int grid = step_resident_workgroups(lds);
-    if (grid < 1) return fail(EMPRISE_EUNSUPPORTED, "step program: no resident workgroup with %zu bytes of LDS", lds);
-    if (!h->step_epoch) {
-        HIP_TRY(hipMalloc(&h->step_epoch, sizeof(uint32_t)));
-        HIP_TRY(hipMalloc(&h->step_err, sizeof(uint32_t)));
-        const uint32_t one = 1, zero = 0;
-        HIP_TRY(hipMemcpy(h->step_epoch, &one, sizeof one, hipMemcpyHostToDevice));
-        HIP_TRY(hipMemcpy(h->step_err, &zero, sizeof zero, hipMemcpyHostToDevice));
-    }
-    StepPhase* prog = nullptr;
-    HIP_TRY(hipMalloc(&prog, h->rec.size() * sizeof(StepPhase)));
-    hipError_t e = hipMemcpy(prog, h->rec.data(), h->rec.size() * sizeof(StepPhase), hipMemcpyHostToDevice);
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-    if (e == hipSuccess) e = hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal);
-    if (e == hipSuccess) {
-        hipError_t le = launch_step(prog, (int)h->rec.size(), h->step_epoch, h->step_err, grid, lds, h->stream);
-        if (le == hipSuccess)
-            le = launch_step_finish(h->fin.key, h->fin.index, h->fin.state, h->fin.prompt, h->fin.history, h->fin.next,
-                                    h->step_epoch, h->stream);
-        e = hipStreamEndCapture(h->stream, &graph);
-        if (le != hipSuccess) e = le;
-    }
-    if (e == hipSuccess) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    if (graph) (void)hipGraphDestroy(graph);
-    if (e != hipSuccess) {
-        (void)hipFree(prog);
-        return fail(EMPRISE_EDEVICE, "step program: %s", hipGetErrorString(e));
-    }
-    const uint64_t id = h->next_graph++;
-    h->graphs.emplace(id, exec);
-    h->program_of.emplace(id, prog);
-    *out = id;
-    return EMPRISE_OK;
-}
-}  // namespace
-
 emprise_status emprise_hip_graph_end(emprise_hip* h, emprise_graph* out) {
     if (!h || !out) return fail(EMPRISE_EINVAL, "null argument");
     if (!h->capturing) return fail(EMPRISE_ESTATE, "not capturing");
-    if (h->recording) {
-        h->recording = false;
-        h->capturing = false;
-        const emprise_status st = finish_program(h, out);
-        rec_reset(h);
-        return st;
-    }
     h->capturing = false;
     hipGraph_t graph = nullptr;
     HIP_TRY(hipStreamEndCapture(h->stream, &graph));
@@ -1619,7 +1199,6 @@ emprise_status emprise_hip_graph_launch(emprise_hip* h, emprise_graph g) {
     auto it = h->graphs.find(g);
     if (it == h->graphs.end()) return fail(EMPRISE_EINVAL, "unknown graph");
     HIP_TRY(hipGraphLaunch(it->second, h->stream));
-    if (h->program_of.count(g)) h->step_launched = true;
     return EMPRISE_OK;
 }
 
@@ -1630,11 +1209,6 @@ emprise_status emprise_hip_graph_destroy(emprise_hip* h, emprise_graph g) {
     HIP_TRY(hipStreamSynchronize(h->stream));
     HIP_TRY(hipGraphExecDestroy(it->second));
     h->graphs.erase(it);
-    auto pit = h->program_of.find(g);
-    if (pit != h->program_of.end()) {
-        HIP_TRY(hipFree(pit->second));
-        h->program_of.erase(pit);
-    }
     return EMPRISE_OK;
 }
 

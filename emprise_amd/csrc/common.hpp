@@ -98,7 +98,7 @@ __device__ __forceinline__ float ubyte_f(uint32_t v, int j) { return (float)((v 
 
 // ---- Gated DeltaNet on 16-lane rows --------------------------------------------------
 //
-// Every GDN kernel (the decode kernels, the step program's phase, the prefill scan) keeps
+// Every GDN kernel (the decode kernels and the prefill scan) keeps
 // a vector of SD = 16*NE columns -- a state row, q, k -- on the 16 lanes of a DPP row,
 // lane j holding columns NE*j .. NE*j + NE-1, so a wave carries four rows side by side.
 // A row sum is NE sequential FMAs per lane, then row16_sum; all the kernels use these

@@ -196,7 +196,6 @@ struct AttnArgs {
     float* partial;  // scratch: [kv_heads][chunks][group][head_dim + 2]
     const float2* rope;  // [context][rotary / 2]: (cos, sin) of pos / base^(2i / rotary)
 };
-constexpr int kAttnChunk = 64;    // positions per partial of the step program's attention
 constexpr int kAttnSub = 16;     // positions per step of attention_kernel's online softmax
 constexpr int kAttnSplit = 64;   // position ranges (workgroups) per KV head of attention_kernel
 // `count` consecutive prompt positions from absolute position `first`: qkv row t at

@@ -1,6 +1,5 @@
-// Streaming dequant-matvec building blocks shared by the per-projection kernels
-// (matvec.hip) and the persistent decode-step kernel (step.hip): the chunked weight
-// layout's per-wave loads and per-unit FP32 arithmetic.
+// Streaming dequant-matvec building blocks of the per-projection kernels (matvec.hip):
+// the chunked weight layout's per-wave loads and per-unit FP32 arithmetic.
 //
 // Arithmetic (FP32 path): weight = (d*sc)*(q-32) for Q6_K (quant.cpp:25-40) and
 // (d*sc)*q - dmin*m for Q4_K (quant.cpp:41-61). A unit's contribution is computed as

@@ -103,7 +103,6 @@ emprise_status emprise_model_open(const emprise_model_options* o, emprise_model*
         opt.fused = o->fused != 0;
         opt.graph = o->graph != 0;
         opt.batch_prefill_min = o->batch_prefill < 0 ? 0 : o->batch_prefill == 0 ? 64 : static_cast<size_t>(o->batch_prefill);
-        opt.step_program = o->step_program != 0;
         auto m = std::make_unique<emprise_model>();
         m->model = std::make_unique<emprise::Model>(opt);
         m->name = m->model->backend_name();
@@ -181,7 +180,6 @@ void emprise_model_close(emprise_model* m) { delete m; }
 
 const char* emprise_model_backend_name(const emprise_model* m) { return m ? m->name.c_str() : ""; }
 
-int emprise_model_step_program(const emprise_model* m) { return m ? m->model->step_program() : -1; }
 
 emprise_status emprise_model_get_info(const emprise_model* m, emprise_model_info* info) {
     if (!m || !info) {
@@ -311,6 +309,14 @@ emprise_status emprise_model_generate(emprise_model* m, const int* prompt, size_
         if (arrivals) std::memcpy(arrivals, arr.data(), arr.size() * sizeof(double));
         *emitted = out.size();
     });
+}
+
+emprise_status emprise_model_get_profile(const emprise_model* m, emprise_model_profile* out) {
+    if (!m || !out) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] { *out = m->model->profile(); });
 }
 
 emprise_status emprise_model_trace_step(emprise_model* m, int token, emprise_hip_trace_record* records, size_t cap,

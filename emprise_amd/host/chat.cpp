@@ -153,7 +153,6 @@ int main(int argc, char** argv) {
             else if (arg == "--unfused") opt.fused = 0;
             else if (arg == "--no-graph") opt.graph = 0;
             else if (arg == "--no-batch-prefill") opt.batch_prefill = -1;
-            else if (arg == "--step-program") opt.step_program = 1;
             else if (arg == "--cpu") throw std::invalid_argument("--cpu: this build runs on the MI355X backend only");
             else throw std::invalid_argument("Unknown option: " + arg);
         }
@@ -161,7 +160,7 @@ int main(int argc, char** argv) {
             throw std::invalid_argument("Usage: emprise-chat --model MODEL.gguf (--prompt TEXT | --prompt-file FILE | "
                                         "--prompt-ids 1,2,3 | --synthetic-prompt N [--seed S]) [--raw] [--tokenize] "
                                         "[--tokens N] [--context N] [--fast-q8] [--report FILE] [--unfused] "
-                                        "[--no-graph] [--no-batch-prefill] [--step-program]");
+                                        "[--no-graph] [--no-batch-prefill]");
         if (!prompt_file.empty()) {
             std::ifstream f(prompt_file, std::ios::binary);
             if (!f) throw std::runtime_error("Cannot read prompt");
@@ -216,11 +215,27 @@ int main(int argc, char** argv) {
         const double roofline = rate * double(info.token_weight_bytes) / 8.0e12;
         std::cerr << "Load: " << load << "s; first token after load: " << first << "s; generated: " << emitted
                   << "; decode: " << rate << " tokens/s (" << 100.0 * roofline << "% of the 8 TB/s weight roofline)\n";
+        // The profile (chat.cpp:72-76): the decode steps are replayed graphs, so the split by
+        // kind comes from one more step launched eagerly with per-launch event timing after
+        // the output is complete (emprise_model_get_profile), when the context has room.
+        emprise_model_profile prof{};
+        if (!tokens.empty() && prompt.size() + tokens.size() < opt.context) {
+            std::vector<emprise_hip_trace_record> rec(4096);
+            size_t nrec = 0;
+            check(emprise_model_trace_step(m, tokens.back(), rec.data(), rec.size(), &nrec));
+        }
+        check(emprise_model_get_profile(m, &prof));
+        std::cerr << "Matrix work (device kernels, " << prof.traced_steps << " traced step(s) x " << prof.decode_steps
+                  << " decode steps): " << prof.matrix_seconds << "s in " << prof.matrix_calls
+                  << " calls; other work: " << prof.non_matrix_seconds << "s\n";
+        std::cerr << "Non-matrix: norm " << prof.norm_seconds << "s, attention " << prof.attention_seconds
+                  << "s, recurrent " << prof.recurrent_seconds << "s\n";
         if (!report_file.empty()) {
             // The reference's --report fields (chat.cpp:77-84), then this build's roofline.
             // text: the decoded output ("" without a tokenizer). matrix_seconds / matrix_calls /
-            // non_matrix_seconds are the reference's host timers around each backend call;
-            // the device path replays one graph per token and has no such calls: 0.
+            // non_matrix_seconds: the profile above (device kernel time of the decode steps,
+            // split by kind on a traced step; the reference's own device path leaves them at
+            // the prefill's host timers).
             std::ofstream f(report_file);
             if (!f) throw std::runtime_error("Cannot write report");
             f.precision(9);
@@ -230,7 +245,8 @@ int main(int argc, char** argv) {
               << ",\n  \"load_seconds\": " << load
               << ",\n  \"first_token_seconds\": " << first << ",\n  \"generation_tokens_per_second\": " << rate
               << ",\n  \"content_arrivals_seconds\": " << json_list(arrivals)
-              << ",\n  \"matrix_seconds\": 0,\n  \"matrix_calls\": 0,\n  \"non_matrix_seconds\": 0"
+              << ",\n  \"matrix_seconds\": " << prof.matrix_seconds << ",\n  \"matrix_calls\": " << prof.matrix_calls
+              << ",\n  \"non_matrix_seconds\": " << prof.non_matrix_seconds
               << ",\n  \"context\": " << opt.context
               << ",\n  \"quantized_activations\": " << (opt.quantize_activations ? "true" : "false")
               << ",\n  \"fused_ffn\": " << (opt.fused ? "true" : "false")

@@ -329,8 +329,6 @@ emprise_graph Model::step_graph(bool logits) {
     bool& have = logits ? have_graph_full_ : have_graph_prefill_;
     emprise_graph& g = logits ? graph_full_ : graph_prefill_;
     if (!have) {
-        const bool program = opt_.step_program && opt_.fused && step_program_ != 0;
-        hip_check(emprise_hip_set_step_program(backend_->get(), program ? 1 : 0), "step_program");
         backend_->graph_begin();
         try {
             enqueue_step(logits);
@@ -339,26 +337,7 @@ emprise_graph Model::step_graph(bool logits) {
             (void)emprise_hip_graph_end(backend_->get(), &dead);
             throw;
         }
-        emprise_graph rec = 0;
-        const emprise_status st = emprise_hip_graph_end(backend_->get(), &rec);
-        if (program && st == EMPRISE_EUNSUPPORTED) {
-            // a call or shape the step program cannot express: per-op graph instead
-            hip_check(emprise_hip_set_step_program(backend_->get(), 0), "step_program");
-            backend_->graph_begin();
-            try {
-                enqueue_step(logits);
-            } catch (...) {
-                emprise_graph dead = 0;
-                (void)emprise_hip_graph_end(backend_->get(), &dead);
-                throw;
-            }
-            rec = backend_->graph_end();
-            step_program_ = 0;
-        } else {
-            hip_check(st, "graph_end");
-            step_program_ = program ? 1 : 0;
-        }
-        g = rec;
+        g = backend_->graph_end();
         have = true;
     }
     return g;
@@ -371,6 +350,8 @@ std::vector<float> Model::evaluate(int token, bool want_logits) {
     if (opt_.graph) backend_->graph_launch(step_graph(want_logits));
     else enqueue_step(want_logits);
     ++position_;
+    ++evaluated_;
+    if (want_logits) ++decode_steps_;
     std::vector<float> out;
     if (want_logits) {
         out.resize(static_cast<size_t>(info_.vocab));
@@ -386,32 +367,23 @@ std::vector<emprise_hip_trace_record> Model::trace_step(int token) {
     if (token < 0 || token >= info_.vocab) throw std::out_of_range("Token ID");
     set_state(static_cast<int>(position_), token, 0);
     backend_->sync();
-    const emprise_model_info& d = info_;
-    if (opt_.graph && step_program_ == 1) {
-        // the whole step is one persistent kernel (+ the one-thread finish kernel): time
-        // the replay between two events; bytes = every matrix once, the recurrent states
-        // read and written, K/V rows 0..position of the attention layers
-        const emprise_graph g = step_graph(true);
-        constexpr int kA = 65534, kB = 65535;
-        backend_->event(kA);
-        backend_->graph_launch(g);
-        backend_->event(kB);
-        const float ms = backend_->elapsed(kA, kB);
-        uint64_t bytes = d.token_weight_bytes;
-        const uint64_t kd = uint64_t(d.key_heads) * d.state_dim, vd = uint64_t(d.value_heads) * d.state_dim;
-        for (const Layer& L : layers_) {
-            if (L.recurrent) bytes += 2 * (vd * d.state_dim * 4 + (2 * kd + vd) * d.conv_width * 4);
-            else bytes += uint64_t(position_ + 1) * d.kv_heads * d.head_dim * 4 * 2;
-        }
-        ++position_;
-        return {emprise_hip_trace_record{"decode_step", bytes, ms}};
-    }
     hip_check(emprise_hip_trace_begin(backend_->get()), "trace_begin");
     enqueue_step(true);
     std::vector<emprise_hip_trace_record> rec(4096);
     size_t n = 0;
     hip_check(emprise_hip_trace_end(backend_->get(), rec.data(), rec.size(), &n), "trace_end");
     rec.resize(n);
+    // the step's kernel time by kind, for profile()
+    step_matrix_ms_ = step_norm_ms_ = step_attention_ms_ = step_recurrent_ms_ = step_other_ms_ = 0;
+    for (const auto& r : rec) {
+        const std::string k = r.kernel;
+        if (k.rfind("matvec", 0) == 0 || k.rfind("gemm", 0) == 0) step_matrix_ms_ += r.ms;
+        else if (k == "rmsnorm" || k == "add_rmsnorm") step_norm_ms_ += r.ms;
+        else if (k.rfind("attention", 0) == 0) step_attention_ms_ += r.ms;
+        else if (k.rfind("gdn", 0) == 0 || k == "delta_conv") step_recurrent_ms_ += r.ms;
+        else step_other_ms_ += r.ms;
+    }
+    ++traced_steps_;  // a measurement: not counted as an evaluated token or decode step
     // attention reads K and V rows 0..position of its layer
     const uint64_t kv = uint64_t(position_ + 1) * info_.kv_heads * info_.head_dim * 4 * 2;
     for (auto& r : rec)
@@ -516,6 +488,7 @@ std::vector<std::vector<float>> Model::evaluate_block(const std::vector<int>& to
     std::vector<float> flat;
     prefill_batched(start, n, &flat);
     position_ = start + n;
+    evaluated_ += n;
     const size_t V = static_cast<size_t>(info_.vocab);
     out.reserve(n);
     for (size_t i = 0; i < n; ++i)
@@ -670,6 +643,8 @@ std::vector<int> Model::generate(const std::vector<int>& prompt, size_t count, s
         backend_->event(static_cast<int>(1 + i));
     }
     backend_->sync();
+    evaluated_ += static_cast<uint64_t>(n - 1) + count;
+    decode_steps_ += count;
     std::vector<int> hist(count);
     backend_->dev_download(hist.data(), dev_history_ + static_cast<uint64_t>(n - 1) * sizeof(int), count * sizeof(int));
     std::vector<int> out;
@@ -723,8 +698,31 @@ std::vector<float> Model::prefill(const std::vector<int>& tokens, bool want_logi
             }
         }
         position_ = start + n - 1;
+        evaluated_ += n - 1;
     }
     return evaluate(tokens[n - 1], want_logits);
+}
+
+// Model::profile (model.hpp:21-25); see emprise_model_get_profile in emprise_host.h.
+emprise_model_profile Model::profile() const {
+    emprise_model_profile p{};
+    p.evaluated_tokens = evaluated_;
+    p.decode_steps = decode_steps_;
+    p.traced_steps = traced_steps_;
+    // projections per decode step, one per weight as the reference counts them (mms and mm,
+    // model.cpp:90-115; feed_forward as 3, model.cpp:236)
+    uint64_t per_step = 1;  // the output head
+    for (const Layer& L : layers_) per_step += L.recurrent ? 5 + 3 : 4 + 3;
+    p.matrix_calls = per_step * decode_steps_;
+    if (traced_steps_) {
+        const double s = 1e-3 * static_cast<double>(decode_steps_);
+        p.matrix_seconds = step_matrix_ms_ * s;
+        p.norm_seconds = step_norm_ms_ * s;
+        p.attention_seconds = step_attention_ms_ * s;
+        p.recurrent_seconds = step_recurrent_ms_ * s;
+        p.non_matrix_seconds = (step_norm_ms_ + step_attention_ms_ + step_recurrent_ms_ + step_other_ms_) * s;
+    }
+    return p;
 }
 
 }  // namespace emprise

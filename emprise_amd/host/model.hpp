@@ -25,8 +25,6 @@ struct ModelOptions {
     bool graph = true;
     // prompts of at least this many tokens prefill in batches (GEMM projections); 0 = never
     size_t batch_prefill_min = 64;
-    // replay decode steps as one persistent kernel when the backend can record them
-    bool step_program = false;
 };
 
 class Model {
@@ -46,6 +44,7 @@ public:
     std::vector<float> evaluate(int token, bool want_logits = true);
     std::vector<float> last_hidden();
     std::vector<emprise_hip_trace_record> trace_step(int token);
+    emprise_model_profile profile() const;
     // prefill + greedy loop; arrivals[i] = seconds from the first launch to token i
     std::vector<int> generate(const std::vector<int>& prompt, size_t count, std::vector<double>* arrivals);
     // Model::prefill: tokens from the current position on; the last one's logits
@@ -94,6 +93,10 @@ private:
     emprise_dev dev_state_ = 0, dev_next_ = 0, dev_prompt_ = 0, dev_history_ = 0;
     int last_x_ = 0;  // residual buffer holding the stream after the last step
     size_t position_ = 0;
+    // Model::profile: positions evaluated and decode steps run since open, and the per-step
+    // kernel time by kind (ms) from the last traced step
+    uint64_t evaluated_ = 0, decode_steps_ = 0, traced_steps_ = 0;
+    double step_matrix_ms_ = 0, step_norm_ms_ = 0, step_attention_ms_ = 0, step_recurrent_ms_ = 0, step_other_ms_ = 0;
     emprise_graph graph_full_ = 0, graph_prefill_ = 0;
     // batched prefill buffers, sized for pf_rows_ tokens on first use
     size_t pf_rows_ = 0;
@@ -110,12 +113,7 @@ private:
         size_t length = 0;
         emprise_dev cat = 0, cur = 0, x = 0, in = 0, ctl = 0;
     } mtp_;
-    int step_program_ = -1;  // 1: step graphs are persistent programs, 0: per-op graphs, -1: none yet
 
-public:
-    int step_program() const { return step_program_; }
-
-private:
 };
 
 }  // namespace emprise

@@ -3,7 +3,8 @@
 
 #include <algorithm>
 #include <cstdint>
-#include <limits>
+#include <functional>
+#include <queue>
 #include <stdexcept>
 
 #include "gguf.hpp"
@@ -153,106 +154,158 @@ std::vector<size_t> pretokenize(const std::string& text) {
     return ends;
 }
 
-Tokenizer::Tokenizer(const Gguf& g) {
-    const MetaValue* model = g.meta("tokenizer.ggml.model");
-    const MetaValue* pre = g.meta("tokenizer.ggml.pre");
-    if (!model || model->text != "gpt2" || !pre || pre->text != "qwen35")
-        throw std::runtime_error("Tokenizer currently supports qwen35 GPT-2 BPE only");
-    const MetaValue* tokens = g.meta("tokenizer.ggml.tokens");
-    const MetaValue* types = g.meta("tokenizer.ggml.token_type");
-    const MetaValue* merges = g.meta("tokenizer.ggml.merges");
-    if (!tokens || !types || !merges || tokens->array_type != 8 || merges->array_type != 8 ||
-        types->integers.size() != types->array_len)
-        throw std::runtime_error("Missing tokenizer metadata");
-    if (types->integers.size() != tokens->strings.size()) throw std::runtime_error("Vocabulary/type size mismatch");
-    for (size_t i = 0; i < merges->strings.size(); ++i) rank_.emplace(merges->strings[i], static_cast<int>(i));
-    // GPT-2's byte encoder: printable Latin-1 bytes stand for themselves, the others map
-    // to U+0100 on in byte order (tokenizer.cpp:68-74)
-    std::unordered_map<uint32_t, uint8_t> reverse;
-    uint32_t extra = 256;
-    for (int b = 0; b < 256; ++b) {
-        const bool direct = (b >= 33 && b <= 126) || (b >= 161 && b <= 172) || b >= 174;
-        const uint32_t c = direct ? static_cast<uint32_t>(b) : extra++;
-        byte_encoder_[b] = utf8(c);
-        reverse[c] = static_cast<uint8_t>(b);
+// The byte-level alphabet of GPT-2 BPE: a byte whose Latin-1 character is printable and
+// not a space ('!'..'~', U+00A1..U+00AC, U+00AE..U+00FF) is written as that character;
+// the other 68 bytes, taken in increasing order, are written as U+0100, U+0101, ... so
+// every byte has a visible single-code-point spelling.
+std::array<uint32_t, 256> byte_alphabet() {
+    std::array<uint32_t, 256> cp{};
+    uint32_t spare = 0x100;
+    for (uint32_t b = 0; b < 256; ++b) {
+        const bool printable = (b >= 0x21 && b <= 0x7E) || (b >= 0xA1 && b <= 0xAC) || b >= 0xAE;
+        cp[b] = printable ? b : spare++;
     }
-    const auto& vocab = tokens->strings;
-    decoded_.reserve(vocab.size());
-    for (size_t i = 0; i < vocab.size(); ++i) {
-        const std::string& token = vocab[i];
-        ids_.emplace(token, static_cast<int>(i));
-        const int64_t type = types->integers[i];
-        if (type == 3 || type == 4) {
-            special_.emplace_back(token, static_cast<int>(i));
-            decoded_.push_back(token);
-            continue;
-        }
-        std::string bytes;
-        for (size_t pos = 0; pos < token.size();) {
-            uint32_t c;
-            const size_t len = next_utf8(token, pos, c);
-            if (!len) throw std::runtime_error("Invalid vocabulary UTF-8");
-            const auto it = reverse.find(c);
-            if (it == reverse.end()) {  // not byte-encoded: an unused vocabulary entry
-                bytes = token;
-                break;
-            }
-            bytes.push_back(static_cast<char>(it->second));
-            pos += len;
-        }
-        decoded_.push_back(std::move(bytes));
-    }
+    return cp;
 }
 
+Tokenizer::Tokenizer(const Gguf& g) {
+    const MetaValue* kind = g.meta("tokenizer.ggml.model");
+    const MetaValue* pre = g.meta("tokenizer.ggml.pre");
+    if (!kind || kind->text != "gpt2" || !pre || pre->text != "qwen35")
+        throw std::runtime_error("tokenizer: only qwen35 GPT-2 BPE vocabularies are supported");
+    const MetaValue* vocab = g.meta("tokenizer.ggml.tokens");
+    const MetaValue* kinds = g.meta("tokenizer.ggml.token_type");
+    const MetaValue* merges = g.meta("tokenizer.ggml.merges");
+    if (!vocab || !kinds || !merges || vocab->array_type != 8 || merges->array_type != 8 ||
+        kinds->integers.size() != kinds->array_len)
+        throw std::runtime_error("tokenizer: tokens, token types or merges missing from the metadata");
+    if (kinds->integers.size() != vocab->strings.size())
+        throw std::runtime_error("tokenizer: token and token-type arrays differ in length");
+
+    // merge rank = index in the merges list ("left right", one space)
+    rank_.reserve(merges->strings.size());
+    for (size_t r = 0; r < merges->strings.size(); ++r) rank_.emplace(merges->strings[r], static_cast<int>(r));
+
+    const std::array<uint32_t, 256> alphabet = byte_alphabet();
+    std::unordered_map<uint32_t, uint8_t> byte_of;
+    for (int b = 0; b < 256; ++b) {
+        byte_encoder_[b] = utf8(alphabet[b]);
+        byte_of.emplace(alphabet[b], static_cast<uint8_t>(b));
+    }
+
+    // id of every vocabulary string; the bytes each id decodes to. Control (3) and
+    // user-defined (4) tokens are matched and decoded as their literal text; an ordinary
+    // entry that is not spelled in the byte alphabet decodes as its own text too.
+    const auto& words = vocab->strings;
+    ids_.reserve(words.size());
+    decoded_.resize(words.size());
+    for (size_t id = 0; id < words.size(); ++id) {
+        const std::string& w = words[id];
+        ids_.emplace(w, static_cast<int>(id));
+        const int64_t kind_id = kinds->integers[id];
+        if (kind_id == 3 || kind_id == 4) {
+            special_.emplace_back(w, static_cast<int>(id));
+            decoded_[id] = w;
+            continue;
+        }
+        std::string raw;
+        bool in_alphabet = true;
+        for (size_t at = 0; at < w.size() && in_alphabet;) {
+            uint32_t c = 0;
+            const size_t len = next_utf8(w, at, c);
+            if (!len) throw std::runtime_error("tokenizer: a vocabulary entry is not well-formed UTF-8");
+            const auto hit = byte_of.find(c);
+            in_alphabet = hit != byte_of.end();
+            if (in_alphabet) raw.push_back(static_cast<char>(hit->second));
+            at += len;
+        }
+        decoded_[id] = in_alphabet ? std::move(raw) : w;
+    }
+    // longest first, so the first special token that matches at a position is its longest
+    std::stable_sort(special_.begin(), special_.end(),
+                     [](const auto& x, const auto& y) { return x.first.size() > y.first.size(); });
+}
+
+// Byte-pair merging of one pre-tokenized piece. The piece starts as its bytes in the byte
+// alphabet; the merge of lowest rank among all adjacent symbol pairs is applied, to the
+// leftmost such pair, until no adjacent pair has a rank. Symbols sit in a doubly linked
+// list in their original order; candidate pairs wait in a min-heap ordered by (rank,
+// position of the left symbol), and a popped candidate is skipped when either symbol has
+// changed since it was pushed.
 void Tokenizer::ordinary(const std::string& text, std::vector<int>& out) const {
+    struct Sym {
+        std::string s;
+        int prev, next;
+        uint32_t version;  // bumped on every change, invalidating queued pairs
+    };
+    struct Cand {
+        int rank, left;
+        uint32_t vl, vr;
+        bool operator>(const Cand& o) const { return rank != o.rank ? rank > o.rank : left > o.left; }
+    };
     size_t start = 0;
     for (size_t end : pretokenize(text)) {
-        std::vector<std::string> pieces;
-        for (size_t i = start; i < end; ++i) pieces.push_back(byte_encoder_[static_cast<uint8_t>(text[i])]);
-        // the lowest-ranked adjacent pair merges first, the leftmost of equal pairs
-        while (pieces.size() > 1) {
-            int best_rank = std::numeric_limits<int>::max();
-            size_t best = pieces.size();
-            for (size_t i = 0; i + 1 < pieces.size(); ++i) {
-                const auto found = rank_.find(pieces[i] + ' ' + pieces[i + 1]);
-                if (found != rank_.end() && found->second < best_rank) {
-                    best_rank = found->second;
-                    best = i;
-                }
-            }
-            if (best == pieces.size()) break;
-            pieces[best] += pieces[best + 1];
-            pieces.erase(pieces.begin() + static_cast<std::ptrdiff_t>(best + 1));
+        const int n = static_cast<int>(end - start);
+        std::vector<Sym> sym(static_cast<size_t>(n));
+        for (int i = 0; i < n; ++i)
+            sym[i] = {byte_encoder_[static_cast<uint8_t>(text[start + static_cast<size_t>(i)])], i - 1,
+                      i + 1 < n ? i + 1 : -1, 0};
+        std::priority_queue<Cand, std::vector<Cand>, std::greater<Cand>> heap;
+        auto offer = [&](int l) {
+            const int r = l >= 0 ? sym[l].next : -1;
+            if (l < 0 || r < 0) return;
+            const auto hit = rank_.find(sym[l].s + ' ' + sym[r].s);
+            if (hit != rank_.end()) heap.push({hit->second, l, sym[l].version, sym[r].version});
+        };
+        for (int i = 0; i + 1 < n; ++i) offer(i);
+        while (!heap.empty()) {
+            const Cand c = heap.top();
+            heap.pop();
+            const int r = sym[c.left].next;
+            if (r < 0 || sym[c.left].version != c.vl || sym[r].version != c.vr || sym[c.left].s.empty()) continue;
+            // merge r into its left neighbour
+            sym[c.left].s += sym[r].s;
+            ++sym[c.left].version;
+            sym[r].s.clear();
+            ++sym[r].version;
+            sym[c.left].next = sym[r].next;
+            if (sym[r].next >= 0) sym[sym[r].next].prev = c.left;
+            offer(sym[c.left].prev);
+            offer(c.left);
         }
-        for (const auto& piece : pieces) {
-            const auto found = ids_.find(piece);
-            if (found == ids_.end()) throw std::runtime_error("BPE piece missing from vocabulary");
-            out.push_back(found->second);
+        for (int i = n ? 0 : -1; i >= 0; i = sym[i].next) {
+            const auto hit = ids_.find(sym[i].s);
+            if (hit == ids_.end()) throw std::runtime_error("tokenizer: a merged piece has no vocabulary id");
+            out.push_back(hit->second);
         }
         start = end;
     }
 }
 
+// Special tokens are taken where they occur in the text (the earliest occurrence first,
+// the longest token where several start at one byte); the text between them goes through
+// the pre-tokenizer and the merges.
 std::vector<int> Tokenizer::encode(const std::string& text, bool parse_special) const {
     std::vector<int> out;
-    size_t offset = 0;
-    while (offset < text.size()) {
-        size_t next = text.size(), length = 0;
-        int id = -1;
-        if (parse_special)
-            for (const auto& [s, token] : special_) {
-                const size_t pos = text.find(s, offset);
-                if (pos < next || (pos == next && s.size() > length)) {
-                    next = pos;
-                    length = s.size();
-                    id = token;
-                }
+    size_t plain = 0;  // start of the text not yet encoded
+    if (parse_special && !special_.empty()) {
+        for (size_t at = 0; at < text.size();) {
+            int hit = -1;
+            for (size_t k = 0; k < special_.size() && hit < 0; ++k) {
+                const std::string& w = special_[k].first;
+                if (!w.empty() && text.compare(at, w.size(), w) == 0) hit = static_cast<int>(k);
             }
-        ordinary(text.substr(offset, next - offset), out);
-        if (id < 0) break;
-        out.push_back(id);
-        offset = next + length;
+            if (hit < 0) {
+                ++at;
+                continue;
+            }
+            ordinary(text.substr(plain, at - plain), out);
+            out.push_back(special_[static_cast<size_t>(hit)].second);
+            at += special_[static_cast<size_t>(hit)].first.size();
+            plain = at;
+        }
     }
+    ordinary(text.substr(plain), out);
     return out;
 }
 
@@ -261,8 +314,12 @@ std::string Tokenizer::decode(int token) const {
     return decoded_[static_cast<size_t>(token)];
 }
 
+// The single-turn template (tokenizer.cpp:136-139): the user turn, then an assistant turn
+// that opens with an empty thinking block.
 std::string Tokenizer::chat_prompt(const std::string& user) const {
-    return "<|im_start|>user\n" + user + "<|im_end|>\n<|im_start|>assistant\n<think>\n\n</think>\n\n";
+    static const std::string open = "<|im_start|>user\n";
+    static const std::string close = "<|im_end|>\n<|im_start|>assistant\n<think>\n\n</think>\n\n";
+    return open + user + close;
 }
 
 }  // namespace emprise

@@ -40,8 +40,7 @@ typedef enum {
     EMPRISE_EINVAL = 1,  /* bad argument or shape  (reference: std::invalid_argument) */
     EMPRISE_EDEVICE = 2, /* HIP runtime failure     (reference: runtime_error from check()) */
     EMPRISE_ENOMEM = 3,  /* over the weight budget or out of device memory */
-    EMPRISE_ESTATE = 4,  /* call not allowed in the current state (e.g. during capture) */
-    EMPRISE_EUNSUPPORTED = 5 /* a recorded step program cannot express the call sequence */
+    EMPRISE_ESTATE = 4   /* call not allowed in the current state (e.g. during capture) */
 } emprise_status;
 
 /* GGUF tensor encodings (gguf.hpp:12 WeightType). */
@@ -211,7 +210,7 @@ emprise_status emprise_hip_delta_net(emprise_hip* h, const emprise_hip_delta_net
  * for emprise_hip_delta_net, and gets the same results bit for bit. Every call on one
  * GPU shares that array: calls that overlap on one GPU (several streams or handles)
  * race. Each call writes all the channels it reads before reading them, so nothing
- * needs clearing between calls. Not recordable into step programs (EMPRISE_ESTATE). */
+ * needs clearing between calls. */
 emprise_status emprise_hip_delta_net_noalloc(emprise_hip* h, const emprise_hip_delta_net_params* p);
 /* Backend::delta_net over `count` consecutive positions, for the batched prompt prefill
  * (the reference runs it position by position inside its 4-position prefill batches,
@@ -295,21 +294,6 @@ emprise_status emprise_hip_graph_begin(emprise_hip* h);
 emprise_status emprise_hip_graph_end(emprise_hip* h, emprise_graph* out);
 emprise_status emprise_hip_graph_launch(emprise_hip* h, emprise_graph g);
 emprise_status emprise_hip_graph_destroy(emprise_hip* h, emprise_graph g);
-
-/* Persistent decode-step programs (no reference counterpart). With the mode on,
- * graph_begin .. graph_end records the calls in between -- embed, recurrent,
- * linear_norm, linear, attention, feed_forward, lm_head, advance, with chunked Q6_K /
- * Q4_K weights (cols a multiple of 4096) and FP32 activations -- as the phases of ONE
- * persistent kernel plus a one-thread finish kernel, instead of one launch per op.
- * The returned graph runs that pair. An output that a later call of the same
- * recording reads is handed over in device slots of the backend and is not stored to
- * the caller's buffer; every other output is. graph_end returns EMPRISE_EUNSUPPORTED (and
- * records nothing) when a call or shape falls outside the program's phases; the
- * caller then records the same calls with the mode off. Phases hand activations to
- * each other through tagged device slots, never through a grid-wide barrier; every
- * wait is bounded, and a step whose wait ran out of time makes the next
- * emprise_hip_sync / emprise_hip_download return EMPRISE_EDEVICE. */
-emprise_status emprise_hip_set_step_program(emprise_hip* h, int enable);
 
 /* ---- timing (HIP events on the backend stream) ----------------------------------- */
 /* Records event `slot` (0 <= slot < 65536, created on first use) on the backend

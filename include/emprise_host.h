@@ -38,9 +38,6 @@ typedef struct {
     int graph;                     /* 1: replay the decode step as a hipGraph (default) */
     int batch_prefill;             /* prompts with at least this many tokens before the last one
                                       prefill in batches (GEMM projections); 0 = 64, < 0 = never */
-    int step_program;              /* 1: the graph replays each decode step as one persistent kernel
-                                      (emprise_hip_set_step_program) when the shapes allow; 0 (default):
-                                      one graph node per op */
 } emprise_model_options;
 
 typedef struct emprise_model emprise_model;
@@ -61,9 +58,28 @@ typedef struct {
     double load_seconds;
 } emprise_model_info;
 emprise_status emprise_model_get_info(const emprise_model* m, emprise_model_info* info);
-/* 1 when decode steps run as a persistent step program, 0 when as per-op graphs (known
- * after the first graph replay; -1 before). */
-int emprise_model_step_program(const emprise_model* m);
+
+/* Model::profile (model.hpp:21-25): the reference times every backend call on its host
+ * path (model.cpp:90-115, :216-256) and, on its device path (evaluate_device,
+ * model.cpp:422-472), counts evaluated tokens only. Here a decode step is one replayed
+ * graph, so its split by kind comes from the per-launch HIP event timing of the last
+ * emprise_model_trace_step (one eager step), scaled by the decode steps run since the model
+ * was opened (traced steps themselves are measurements and are not counted); with no traced
+ * step the times are 0. matrix_* covers the projection kernels
+ * (matvec, GEMM), matrix_calls counts projections the reference's way (one per weight:
+ * q/k/v/o or qkv/gate/alpha/beta/out, gate/up/down, the output head), norm_* the
+ * stand-alone RMSNorm kernels (the fused path folds RMSNorm into the projections' input
+ * staging, so 0 there), attention_* / recurrent_* the attention and Gated DeltaNet
+ * kernels, and non_matrix_* everything but the projections. Batched prefills add their
+ * positions to evaluated_tokens only. */
+typedef struct {
+    double matrix_seconds, non_matrix_seconds;
+    double norm_seconds, attention_seconds, recurrent_seconds;
+    uint64_t matrix_calls, evaluated_tokens;
+    uint64_t decode_steps;  /* single-position steps with the output head since open */
+    uint64_t traced_steps;  /* steps the per-kind split was measured on (0: none yet) */
+} emprise_model_profile;
+emprise_status emprise_model_get_profile(const emprise_model* m, emprise_model_profile* out);
 
 /* Model::reset (model.cpp:479). */
 emprise_status emprise_model_reset(emprise_model* m);

@@ -16,8 +16,8 @@ Outputs (tests/golden/):
   c4a_9b_q4km.json   2048-token prompt (seed 1) + 16 greedy tokens and margins
   c4a_9b_q4km.npz    logits after the last prompt position
   c4b_9b_q4km_q8.json  --fast-q8 (every Q6_K projection on round(x/s)*fp16(s) inputs,
-                     core.cpp:119-125): 32-token prompt (seed 2) + 32 greedy tokens,
-                     margins, top-1/top-2 logits
+                     core.cpp:119-125): 512-token prompt (seed 2) + 256 greedy tokens,
+                     margins, top-1/top-2 logits and the top-2 index
   c4b_9b_q4km_q8.npz   logits after the last prompt position
 
 Usage: python tests/golden/make_golden_9b.py [c4b] [c3] [c4a]   (all by default)
@@ -84,18 +84,21 @@ def run(path: Path, prompt, count: int, fast_q8: bool):
         logits = m.evaluate_many(chunk, logits=(start + len(chunk) == len(prompt)))
         print(f"  prompt {start + len(chunk)}/{len(prompt)} ({time.time() - t0:.0f}s)", flush=True)
     prompt_logits = logits.copy()
-    tokens, margins, v1s, v2s = [], [], [], []
+    tokens, margins, v1s, v2s, seconds = [], [], [], [], []
     for i in range(count):
         tok, v1, v2 = top2(logits)
+        rest = logits.copy()
+        rest[tok] = -np.inf
         tokens.append(tok)
         margins.append(v1 - v2)
         v1s.append(v1)
         v2s.append(v2)
+        seconds.append(int(np.argmax(rest)))
         if i + 1 < count:
             logits = m.evaluate(tok)
     m.close()
     print(f"  done in {time.time() - t0:.0f}s", flush=True)
-    return prompt_logits, {"tokens": tokens, "margins": margins, "top1": v1s, "top2": v2s}
+    return prompt_logits, {"tokens": tokens, "margins": margins, "top1": v1s, "top2": v2s, "second": seconds}
 
 
 def main():
@@ -105,7 +108,7 @@ def main():
     cases = {
         "c3": ("9b_q6k", 0, 512, 128, False, "c3_9b_q6k"),
         "c4a": ("9b_q4km", 1, 2048, 16, False, "c4a_9b_q4km"),
-        "c4b": ("9b_q4km", 2, 32, 32, True, "c4b_9b_q4km_q8"),
+        "c4b": ("9b_q4km", 2, 512, 256, True, "c4b_9b_q4km_q8"),
     }
     for name in which:
         kind, pseed, plen, count, q8, out = cases[name]

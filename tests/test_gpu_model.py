@@ -52,7 +52,9 @@ def test_tiny_generate_matches_oracle(tiny_path, fused, graph):
     assert np.all(np.diff(arrivals) >= 0)
     checked = _greedy_agreement(tokens, ref_tokens, margins)
     print(f"greedy tokens identical over {checked} of 64 positions")
-    assert checked >= 8
+    # every one of the seeded prompt's 64 CPU picks has a top-2 margin above 1e-3, so all
+    # 64 are compared
+    assert min(margins[:64]) > MARGIN and checked == 64
 
 
 @pytest.mark.parametrize("n_prompt,count,context", [(200, 64, 512), (2100, 16, 4096)])
@@ -215,6 +217,11 @@ def test_chat_cli_report(tmp_path):
     assert rep["prompt_tokens"] == prompt and rep["context"] == 512 and rep["fused_ffn"] is True
     assert len(rep["content_arrivals_seconds"]) == len(rep["output_tokens"]) == 16
     assert rep["generation_tokens_per_second"] > 0
+    # the profile (chat.cpp:72-84): 16 decode steps, each 3 recurrent layers x 8 projections +
+    # 1 attention layer x 7 + the output head; times from a traced step, scaled by the steps
+    assert rep["matrix_calls"] == 16 * (3 * 8 + 7 + 1)
+    assert rep["matrix_seconds"] > 0 and rep["non_matrix_seconds"] > 0
+    assert "traced step(s) x 16 decode steps" in r.stderr
     ref_tokens, margins = oracle.Model(str(model), context=512).generate(prompt, 16)
     assert _greedy_agreement(rep["output_tokens"], ref_tokens, margins) >= 8
     assert r.stdout.split() == [str(t) for t in rep["output_tokens"]]
