@@ -23,6 +23,11 @@ F32, F16, Q4_K, Q6_K, BF16 = 0, 1, 12, 14, 30
 OK, EINVAL, EDEVICE, ENOMEM, ESTATE = 0, 1, 2, 3, 4
 
 
+# emprise_trace_fn (include/emprise_host.h): (user, position, name, data, n)
+TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float),
+                            ctypes.c_uint64)
+
+
 class EmpriseError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"[status {status}] {message}")
@@ -457,6 +462,8 @@ def host_lib() -> ctypes.CDLL:
     lib.emprise_model_reset.argtypes = [vp]
     lib.emprise_model_evaluate.restype = ctypes.c_int
     lib.emprise_model_evaluate.argtypes = [vp, ctypes.c_int, P(ctypes.c_float)]
+    lib.emprise_model_set_trace.restype = ctypes.c_int
+    lib.emprise_model_set_trace.argtypes = [vp, TRACE_FN, vp]
     lib.emprise_model_last_hidden.restype = ctypes.c_int
     lib.emprise_model_last_hidden.argtypes = [vp, P(ctypes.c_float)]
     lib.emprise_tokenizer_open.restype = ctypes.c_int
@@ -625,6 +632,21 @@ class Model:
         ptr = out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if logits else None
         _host_check(host_lib().emprise_model_evaluate(self.m, token, ptr))
         return out
+
+    def set_trace(self, hook):
+        """ModelOptions::trace (model.hpp:18-19): hook(position, name, array) is called
+        synchronously by evaluate() at the reference's trace points (attn_norm-L,
+        attn_residual-L, l_out-L, result_norm, logits), with a copy of the tensor; None
+        removes it."""
+        if hook is None:
+            self._trace = None
+            _host_check(host_lib().emprise_model_set_trace(self.m, TRACE_FN(), None))
+            return
+
+        def tramp(_user, position, name, data, n):
+            hook(int(position), name.decode(), np.ctypeslib.as_array(data, shape=(n,)).copy())
+        self._trace = TRACE_FN(tramp)
+        _host_check(host_lib().emprise_model_set_trace(self.m, self._trace, None))
 
     def prefill(self, tokens, logits: bool = True):
         """Model::prefill: tokens from the current position on (batched), the last

@@ -11,8 +11,10 @@
 // also appends the new k/v to the caches and uses them straight from LDS. Each
 // workgroup writes an unnormalised partial (o, running max, sum of exponentials); a
 // second small kernel merges the (at most kAttnSplit) partials, divides, and applies the
-// sigmoid output gate. (A last-workgroup merge inside the first kernel would need
-// device-scope fences, which write back and invalidate a whole L2 on this part.)
+// sigmoid output gate. (A last-workgroup merge inside the first kernel needs
+// agent-scope fences, which write back and invalidate an L2 on this part: measured
+// 29.3 us per call at 512 positions against 9.9 us for the two kernels, and 2.9 us more
+// even at 16 positions, where four workgroups take part.)
 //
 // Inside a workgroup (8 waves) every wave owns kAttnSub/8 positions of each sub-chunk
 // and keeps their K and V rows in registers, lane l holding dims E*l .. E*l+E-1 (head_dim = 64*E,
@@ -23,7 +25,12 @@
 // (16 Q / 4 KV heads x 256; one attention + merge, replayed from a graph): 10.3, 13.4
 // and 17.5 µs at 512, 2048 and 4096 positions, against 11.6, 16.2 and 23.0 µs with
 // 4-wave workgroups and 14.8, 15.1 and 18.4 µs for the earlier design (64-position
-// chunks, one workgroup each, keys staged in LDS, one score per lane).
+// chunks, one workgroup each, keys staged in LDS, one score per lane); 9.1, 11.4 and
+// 15.7 µs for this kernel on a later box. Measured alternatives that did not pay, same
+// box each: computing the RoPE angles in the kernel instead of reading the table (9.9
+// against 9.2 µs at 512), issuing the norm-input loads before the position read (9.13
+// against 9.10), loading each range's first K/V rows before the position is known
+// (no gain, and the ranges past the position then read rows they never use).
 //
 // The grid does not depend on the position, so the launch can be replayed from a
 // hipGraph: the position is read from device memory and ranges past it return at once.
@@ -345,7 +352,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
 // each wave's share of the o values (ranges w, w+4, ...), the statistics -- goes out
 // together with the position's, before it is known which ranges hold positions (the
 // slots of the others are loaded but never used); the four waves' sums are added
-// through LDS.
+// through LDS. Loading only the ranges that hold positions makes those loads wait for
+// the position read: measured 1.2 us slower per call at 512 positions and 2.3 us at
+// 1024-4096 (graph replay), for half the merge's fetched bytes at 512.
 constexpr int kCombineBatch = kAttnSplit / 4;  // ranges per wave
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
     __shared__ float wts[kAttnSplit];

@@ -209,6 +209,14 @@ emprise_status emprise_model_evaluate(emprise_model* m, int token, float* logits
     });
 }
 
+emprise_status emprise_model_set_trace(emprise_model* m, emprise_trace_fn fn, void* user) {
+    if (!m) {
+        g_error = "null argument";
+        return EMPRISE_EINVAL;
+    }
+    return guarded([&] { m->model->set_trace(fn, user); });
+}
+
 emprise_status emprise_model_prefill(emprise_model* m, const int* tokens, size_t n, float* logits) {
     if (!m || (!tokens && n)) {
         g_error = "null argument";

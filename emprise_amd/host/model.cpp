@@ -222,7 +222,17 @@ void Model::set_state(int position, int token, int prompt_len) {
 
 // One position. Token and position come from dev_state_ = {position, token,
 // prompt_len}; the last call advances them on the device.
-void Model::enqueue_step(bool logits) {
+// Copies n floats of src to the host and calls the trace hook with them under `name` at
+// the current position (ModelOptions::trace, model.cpp:118-120).
+void Model::emit(const char* name, emprise_dev src, uint64_t n, std::vector<float>* keep) {
+    std::vector<float> local;
+    std::vector<float>& v = keep ? *keep : local;
+    v.resize(static_cast<size_t>(n));
+    backend_->dev_download(v.data(), src, n * 4);
+    trace_fn_(trace_user_, position_, name, v.data(), n);
+}
+
+void Model::enqueue_step(bool logits, bool traced) {
     HipBackend& b = *backend_;
     const emprise_model_info& d = info_;
     const int H = d.hidden;
@@ -272,7 +282,10 @@ void Model::enqueue_step(bool logits) {
         // x_next = x + delta; input = rms(x_next) * norm (model.cpp:217, :226-228, :243, :249).
         int cur = 0;
         emprise_dev pending = 0;
-        for (const Layer& L : layers_) {
+        std::vector<float> xs, ds;  // traced: the stream and the feed-forward output
+        for (size_t l = 0; l < layers_.size(); ++l) {
+            const Layer& L = layers_[l];
+            const std::string n = std::to_string(l);
             emprise_hip_input in{x_[cur], pending, pending ? x_[cur ^ 1] : 0, L.attn_norm, d.eps};
             if (pending) cur ^= 1;
             if (L.recurrent) {
@@ -284,21 +297,42 @@ void Model::enqueue_step(bool logits) {
                 b.dev_attention(attention_params(L), qkv_, attn_out_);
                 b.dev_linear(L.o, attn_out_, delta_attn_);
             }
+            // x_[cur] now holds the block's input stream (its first projection wrote it)
+            if (traced) {
+                b.dev_rmsnorm(x_[cur], L.attn_norm, norm_, H, d.eps);
+                emit(("attn_norm-" + n).c_str(), norm_, H);
+            }
             emprise_hip_input in2{x_[cur], delta_attn_, x_[cur ^ 1], L.post_norm, d.eps};
             cur ^= 1;
             b.dev_ffn(&in2, 0, L.gate, L.up, L.down, delta_ffn_);
             pending = delta_ffn_;
+            if (traced) {
+                emit(("attn_residual-" + n).c_str(), x_[cur], H, &xs);
+                ds.resize(static_cast<size_t>(H));
+                b.dev_download(ds.data(), delta_ffn_, static_cast<uint64_t>(H) * 4);
+                // the add the next projection's staging makes (one FP32 add per element)
+                for (int i = 0; i < H; ++i) xs[static_cast<size_t>(i)] += ds[static_cast<size_t>(i)];
+                trace_fn_(trace_user_, position_, ("l_out-" + n).c_str(), xs.data(), static_cast<uint64_t>(H));
+            }
         }
         if (logits) {
             emprise_hip_input in{x_[cur], pending, x_[cur ^ 1], output_norm_, d.eps};
             last_x_ = cur ^ 1;
             hip_check(emprise_hip_lm_head(b.get(), &in, output_, logits_, dev_next_), "lm_head");
+            if (traced) {
+                b.dev_rmsnorm(x_[cur ^ 1], output_norm_, norm_, H, d.eps);
+                emit("result_norm", norm_, H);
+                emit("logits", logits_, static_cast<uint64_t>(d.vocab));
+            }
         }
     } else {
         // One op per launch, in the order of evaluate_device (model.cpp:422-472).
         const emprise_dev x = x_[0];
-        for (const Layer& L : layers_) {
+        for (size_t l = 0; l < layers_.size(); ++l) {
+            const Layer& L = layers_[l];
+            const std::string n = std::to_string(l);
             b.dev_rmsnorm(x, L.attn_norm, norm_, H, d.eps);
+            if (traced) emit(("attn_norm-" + n).c_str(), norm_, H);
             if (L.recurrent) {
                 const auto p = recurrent_params(L);
                 b.dev_recurrent(p, nullptr, norm_, tmp_);
@@ -310,14 +344,18 @@ void Model::enqueue_step(bool logits) {
                 b.dev_linear(L.o, attn_out_, tmp_);
             }
             b.dev_add(x, tmp_, H);
+            if (traced) emit(("attn_residual-" + n).c_str(), x, H);
             b.dev_rmsnorm(x, L.post_norm, norm_, H, d.eps);
             b.dev_ffn(nullptr, norm_, L.gate, L.up, L.down, tmp_);
             b.dev_add(x, tmp_, H);
+            if (traced) emit(("l_out-" + n).c_str(), x, H);
         }
         if (logits) {
             last_x_ = 0;
             b.dev_rmsnorm(x, output_norm_, norm_, H, d.eps);
+            if (traced) emit("result_norm", norm_, H);
             b.dev_linear(output_, norm_, logits_);
+            if (traced) emit("logits", logits_, static_cast<uint64_t>(d.vocab));
             b.dev_argmax(logits_, d.vocab, dev_next_);
         }
     }
@@ -347,7 +385,8 @@ std::vector<float> Model::evaluate(int token, bool want_logits) {
     if (position_ >= opt_.context) throw std::runtime_error("Context budget exhausted");
     if (token < 0 || token >= info_.vocab) throw std::out_of_range("Token ID");
     set_state(static_cast<int>(position_), token, 0);
-    if (opt_.graph) backend_->graph_launch(step_graph(want_logits));
+    if (trace_fn_) enqueue_step(want_logits, true);
+    else if (opt_.graph) backend_->graph_launch(step_graph(want_logits));
     else enqueue_step(want_logits);
     ++position_;
     ++evaluated_;

@@ -42,6 +42,10 @@ public:
     emprise_model_info info() const { return info_; }
     void reset();
     std::vector<float> evaluate(int token, bool want_logits = true);
+    void set_trace(emprise_trace_fn fn, void* user) {
+        trace_fn_ = fn;
+        trace_user_ = user;
+    }
     std::vector<float> last_hidden();
     std::vector<emprise_hip_trace_record> trace_step(int token);
     emprise_model_profile profile() const;
@@ -72,7 +76,10 @@ private:
     };
     emprise_weight upload(const std::string& name, uint64_t cols, uint64_t rows);
     emprise_weight upload_vector(const std::string& name, uint64_t n);
-    void enqueue_step(bool logits);  // one position, reading token/position from dev_state_
+    // one position, reading token/position from dev_state_; `traced`: eager, with the
+    // trace hook called at the reference's points
+    void enqueue_step(bool logits, bool traced = false);
+    void emit(const char* name, emprise_dev src, uint64_t n, std::vector<float>* keep = nullptr);
     // positions [start, start + count) of the tokens at dev_prompt_ in batches; with
     // logits, every position's output-head row is appended to it (count x vocab)
     void prefill_batched(size_t start, size_t count, std::vector<float>* logits = nullptr);
@@ -92,6 +99,8 @@ private:
     emprise_dev x_[2] = {0, 0}, delta_attn_ = 0, delta_ffn_ = 0, norm_ = 0, tmp_ = 0, qkv_ = 0, attn_out_ = 0, logits_ = 0;
     emprise_dev dev_state_ = 0, dev_next_ = 0, dev_prompt_ = 0, dev_history_ = 0;
     int last_x_ = 0;  // residual buffer holding the stream after the last step
+    emprise_trace_fn trace_fn_ = nullptr;
+    void* trace_user_ = nullptr;
     size_t position_ = 0;
     // Model::profile: positions evaluated and decode steps run since open, and the per-step
     // kernel time by kind (ms) from the last traced step

@@ -86,6 +86,19 @@ emprise_status emprise_model_reset(emprise_model* m);
 /* Model::evaluate (model.cpp:206-259) on the device: one position; logits (vocab
  * floats) may be NULL. */
 emprise_status emprise_model_evaluate(emprise_model* m, int token, float* logits);
+/* ModelOptions::trace (model.hpp:18-19, model.cpp:118-120): a synchronous diagnostic
+ * hook that emprise_model_evaluate calls with the position, a tensor name and the tensor
+ * (valid only during the call) at the reference's points, in its order: per layer L
+ * "attn_norm-L" (the normalised input of the attention / recurrent block),
+ * "attn_residual-L" (the stream after its residual add) and "l_out-L" (after the
+ * feed-forward's), then, when logits are wanted, "result_norm" and "logits"
+ * (model.cpp:219, :227, :244, :250, :253). While a hook is set, evaluate runs its step as
+ * eager launches and copies each tensor to the host at its point (the fused path's
+ * normalised inputs, which its projections compute in their input staging, by a
+ * stand-alone RMSNorm launch); generate and the batched paths do not call it, as the
+ * reference's device path (evaluate_device) does not. fn NULL removes the hook. */
+typedef void (*emprise_trace_fn)(void* user, uint64_t position, const char* name, const float* data, uint64_t n);
+emprise_status emprise_model_set_trace(emprise_model* m, emprise_trace_fn fn, void* user);
 /* Model::prefill (model.cpp:355-366, model.hpp:40-41): evaluates `tokens` from the current
  * position on -- all but the last in batches (GEMM projections, from 64 tokens) or as
  * replayed steps, the last as a decode step -- and writes the last position's logits

@@ -81,6 +81,7 @@ def lib() -> ctypes.CDLL:
         L.eo_model_seek.restype = i32
         L.eo_model_seek.argtypes = [vp, sz]
         L.eo_model_set_quantize_activations.argtypes = [vp, i32]
+        L.eo_model_set_trace.argtypes = [vp, TRACE_FN, vp]
         L.eo_last_error.restype = ctypes.c_char_p
         _lib = L
     return _lib
@@ -195,6 +196,19 @@ def attention(heads, kv_heads, head_dim, rotary, rope_base, eps, q_norm, k_norm,
     return out
 
 
+# eo_trace_fn / emprise_trace_fn: (user, position, name, data, n)
+TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float),
+                            ctypes.c_uint64)
+
+
+def trace_recorder(store: dict):
+    """A trace hook that keeps a copy of every tensor as store[f"{position}.{name}"]
+    (the naming of the reference's tests/fused_check.cpp:21-23)."""
+    def hook(_user, position, name, data, n):
+        store[f"{position}.{name.decode()}"] = np.ctypeslib.as_array(data, shape=(n,)).copy()
+    return TRACE_FN(hook)
+
+
 class Model:
     """The whole CPU decode path over a GGUF file (Model::Impl::evaluate restated)."""
 
@@ -221,6 +235,12 @@ class Model:
 
     def reset(self):
         lib().eo_model_reset(self.m)
+
+    def set_trace(self, store):
+        """ModelOptions::trace: every tensor evaluate() passes the hook is kept in `store`
+        (see trace_recorder); None removes the hook."""
+        self._trace = trace_recorder(store) if store is not None else None
+        lib().eo_model_set_trace(self.m, self._trace if self._trace else TRACE_FN(), None)
 
     def evaluate(self, token: int, logits: bool = True):
         out = np.empty(self.vocab, dtype=np.float32) if logits else None

@@ -430,6 +430,8 @@ struct eo_model {
     float* output_norm;
     float* last_hidden;
     int q8; /* --fast-q8: Q6_K projections see quantised inputs */
+    eo_trace_fn trace;
+    void* trace_user;
     /* the MTP (next-n) block, blk.<layers> (model.cpp:376-397), when the file has one:
      * an attention layer plus the nextn embedding/hidden norms, eh_proj [2H -> H] and the
      * shared head norm; its own K/V cache (mtp_state) and last output (mtp_hidden) */
@@ -798,6 +800,20 @@ static int model_feed_forward(const eo_model* m, const eo_layer* L, const float*
 
 void eo_model_set_quantize_activations(eo_model* m, int on) { m->q8 = on != 0; }
 
+void eo_model_set_trace(eo_model* m, eo_trace_fn fn, void* user) {
+    m->trace = fn;
+    m->trace_user = user;
+}
+
+/* model.cpp:118-120 */
+static void trace_point(const eo_model* m, const char* name, int layer, const float* x, size_t n) {
+    if (!m->trace) return;
+    char full[64];
+    if (layer >= 0) snprintf(full, sizeof full, "%s-%d", name, layer);
+    else snprintf(full, sizeof full, "%s", name);
+    m->trace(m->trace_user, (uint64_t)m->position, full, x, (uint64_t)n);
+}
+
 /* Model::Impl::evaluate (model.cpp:206-259) with the fused feed-forward default. */
 int eo_model_evaluate(eo_model* m, int token, float* logits) {
     if (m->position >= m->context) { set_err("Context budget exhausted"); return -1; }
@@ -821,6 +837,7 @@ int eo_model_evaluate(eo_model* m, int token, float* logits) {
         eo_layer_state* S = &m->state[l];
         memcpy(nrm, x, (size_t)H * sizeof(float));
         eo_rms(nrm, (size_t)H, L->attn_norm, m->eps);
+        trace_point(m, "attn_norm", l, nrm, (size_t)H);
         if (L->recurrent) {
             /* Backend::recurrent_block (backend.cpp:61-77) */
             if ((rc = mlinear(m, L->tqkv, L->qkv, nrm, (size_t)H, b0, (size_t)ch))) break;
@@ -841,16 +858,20 @@ int eo_model_evaluate(eo_model* m, int token, float* logits) {
             if ((rc = mlinear(m, L->to, L->o, b4, (size_t)m->heads * m->head_dim, attn, (size_t)H))) break;
         }
         for (int i = 0; i < H; ++i) x[i] += attn[i];
+        trace_point(m, "attn_residual", l, x, (size_t)H);
         memcpy(nrm, x, (size_t)H * sizeof(float));
         eo_rms(nrm, (size_t)H, L->post_norm, m->eps);
         if ((rc = model_feed_forward(m, L, nrm, attn))) break;
         for (int i = 0; i < H; ++i) x[i] += attn[i];
+        trace_point(m, "l_out", l, x, (size_t)H);
     }
     if (rc == 0) {
         memcpy(m->last_hidden, x, (size_t)H * sizeof(float));
         if (logits) {
             eo_rms(x, (size_t)H, m->output_norm, m->eps);
+            trace_point(m, "result_norm", -1, x, (size_t)H);
             rc = mlinear(m, m->toutput, m->output, x, (size_t)H, logits, (size_t)m->vocab);
+            if (rc == 0) trace_point(m, "logits", -1, logits, (size_t)m->vocab);
         }
         if (rc == 0) ++m->position;
     }

@@ -99,6 +99,12 @@ void eo_model_reset(eo_model* m);
 void eo_model_set_quantize_activations(eo_model* m, int on);
 /* Model::Impl::evaluate (model.cpp:206-259). logits may be NULL. Returns 0 or -1. */
 int eo_model_evaluate(eo_model* m, int token, float* logits);
+/* ModelOptions::trace (model.hpp:18-19, model.cpp:118-120): eo_model_evaluate calls fn
+ * with the position, the tensor's name and the tensor at the reference's points
+ * (model.cpp:219, :227, :244, :250, :253): "attn_norm-L", "attn_residual-L", "l_out-L"
+ * per layer, then "result_norm" and "logits" when logits are asked for. NULL removes it. */
+typedef void (*eo_trace_fn)(void* user, uint64_t position, const char* name, const float* data, uint64_t n);
+void eo_model_set_trace(eo_model* m, eo_trace_fn fn, void* user);
 /* tokens[0..n) from the current position, bit for bit as n eo_model_evaluate calls, with
  * the projections of all n positions computed together (one weight decode per 64
  * positions). logits (optional) are the last position's. Returns 0 or -1. */

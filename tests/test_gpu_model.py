@@ -269,3 +269,50 @@ def _replace_bad_utf8(b: bytes) -> str:
             out.append("\ufffd")
             i += 1
     return "".join(out)
+
+
+def _trace_names(layers):
+    names = []
+    for layer in range(layers):
+        names += [f"attn_norm-{layer}", f"attn_residual-{layer}", f"l_out-{layer}"]
+    return names + ["result_norm", "logits"]
+
+
+@pytest.mark.parametrize("fused,graph", [(True, True), (False, False)])
+def test_tiny_trace_hook_matches_oracle(tiny_path, fused, graph):
+    """ModelOptions::trace (model.hpp:18-19, model.cpp:118-120, :219-253): the device's
+    tensors at the reference's trace points, position by position, against the oracle's
+    at the same points (each within the per-step bar of the logits test above), in the
+    reference's order and naming; evaluate without logits stops after the last l_out.
+    The fused and per-op forms then agree with each other as tests/fused_check.cpp asks."""
+    prompt = synth_prompt(5, TINY["vocab"], 12)
+    ref = oracle.Model(tiny_path, context=512)
+    want = {}
+    ref.set_trace(want)
+    got, order = {}, []
+
+    def hook(pos, name, x):
+        got[f"{pos}.{name}"] = x
+        order.append(f"{pos}.{name}")
+
+    with Model(tiny_path, context=512, fused=fused, graph=graph) as m:
+        m.set_trace(hook)
+        for pos, tok in enumerate(prompt):
+            logits = pos % 4 != 3  # some positions without the output head
+            ref.evaluate(tok, logits)
+            out = m.evaluate(tok, logits)
+            names = _trace_names(TINY["layers"])
+            if not logits:
+                names = names[:-2]
+            assert order[-len(names):] == [f"{pos}.{n}" for n in names]
+            if logits:
+                assert np.array_equal(got[f"{pos}.logits"], out)
+        m.set_trace(None)
+        n_before = len(order)
+        m.evaluate(prompt[0])
+        assert len(order) == n_before  # hook removed
+    assert set(got) == set(want)
+    for key, w in want.items():
+        err = float(np.max(np.abs(got[key].astype(np.float64) - w)))
+        assert err <= 2e-4 * float(np.max(np.abs(w))), f"{key}: max abs err {err:.3e}"
+    ref.close()
