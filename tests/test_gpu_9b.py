@@ -193,3 +193,37 @@ def test_c4b_9b_q4km_fast_q8_teacher_forced():
     assert compared >= len(g["tokens"]) - 8
     assert rel <= 5e-3
     assert worst <= 5e-3
+
+
+def test_c3_9b_trace_layer_by_layer():
+    """The per-tensor trace hook (model.hpp:18-19) at the 9B shape: the first positions of
+    the C3 prompt on the device and in the CPU oracle (run here, on the same GGUF), every
+    traced tensor compared -- attn_norm-L, attn_residual-L and l_out-L of all 32 layers,
+    result_norm and logits. Each within a relative L2 of 1e-4 (the prompt-end logits of
+    the 512-position C3 run are at ~2e-5); the worst tensor and the drift of the residual
+    stream through the layers are printed, which is what the hook is for: finding the
+    layer where two paths part."""
+    import oracle
+    g, _ = _golden("c3_9b_q6k")
+    path = _model_file("9b_q6k", g["gguf_sha256"])
+    prompt = g["prompt"][:4]
+    ref = oracle.Model(path, context=64)
+    want = {}
+    ref.set_trace(want)
+    for t in prompt:
+        ref.evaluate(t, True)
+    ref.close()
+    got = {}
+    with Model(path, context=64) as m:
+        m.set_trace(lambda pos, name, x: got.__setitem__(f"{pos}.{name}", x))
+        for t in prompt:
+            m.evaluate(t)
+    assert set(got) == set(want) and len(want) == len(prompt) * (3 * NINE_B["layers"] + 2)
+    rel = {k: _rel_l2(got[k], w) for k, w in want.items()}
+    worst = max(rel, key=rel.get)
+    last = len(prompt) - 1
+    drift = [rel[f"{last}.l_out-{layer}"] for layer in range(NINE_B["layers"])]
+    print(f"9B trace: {len(rel)} tensors over {len(prompt)} positions, worst {worst} at rel L2 {rel[worst]:.3e}; "
+          f"position {last} l_out rel L2 by layer: " + " ".join(f"{d:.1e}" for d in drift) +
+          f"; logits {rel[f'{last}.logits']:.3e}")
+    assert rel[worst] <= 1e-4, f"{worst}: rel L2 {rel[worst]:.3e}"
