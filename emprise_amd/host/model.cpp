@@ -182,6 +182,8 @@ Model::Model(const ModelOptions& options) : opt_(options) {
     // activations
     const uint64_t wide = std::max<uint64_t>({H, qd + 2 * kvd, uint64_t(d.heads) * d.head_dim, vd});
     for (auto& x : x_) x = backend_->dev_alloc(H * 4);
+    hid_ = backend_->dev_alloc(H * 4);
+    backend_->dev_fill(hid_, 0.f, H);
     delta_attn_ = backend_->dev_alloc(H * 4);
     delta_ffn_ = backend_->dev_alloc(H * 4);
     norm_ = backend_->dev_alloc(wide * 4);
@@ -198,6 +200,7 @@ Model::Model(const ModelOptions& options) : opt_(options) {
     set_state(0, 0, 0);
     enqueue_step(true);
     backend_->sync();
+    backend_->dev_fill(hid_, 0.f, static_cast<size_t>(H));
     reset();
     d.load_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
 }
@@ -316,11 +319,12 @@ void Model::enqueue_step(bool logits, bool traced) {
             }
         }
         if (logits) {
-            emprise_hip_input in{x_[cur], pending, x_[cur ^ 1], output_norm_, d.eps};
-            last_x_ = cur ^ 1;
+            // the head's input staging writes the final stream to hid_, the hidden vector the
+            // reference keeps from positions with logits only (model.cpp:247-251)
+            emprise_hip_input in{x_[cur], pending, hid_, output_norm_, d.eps};
             hip_check(emprise_hip_lm_head(b.get(), &in, output_, logits_, dev_next_), "lm_head");
             if (traced) {
-                b.dev_rmsnorm(x_[cur ^ 1], output_norm_, norm_, H, d.eps);
+                b.dev_rmsnorm(hid_, output_norm_, norm_, H, d.eps);
                 emit("result_norm", norm_, H);
                 emit("logits", logits_, static_cast<uint64_t>(d.vocab));
             }
@@ -351,7 +355,8 @@ void Model::enqueue_step(bool logits, bool traced) {
             if (traced) emit(("l_out-" + n).c_str(), x, H);
         }
         if (logits) {
-            last_x_ = 0;
+            b.dev_fill(hid_, 0.f, H);
+            b.dev_add(hid_, x, H);
             b.dev_rmsnorm(x, output_norm_, norm_, H, d.eps);
             if (traced) emit("result_norm", norm_, H);
             b.dev_linear(output_, norm_, logits_);
@@ -433,13 +438,13 @@ std::vector<emprise_hip_trace_record> Model::trace_step(int token) {
 
 std::vector<float> Model::last_hidden() {
     std::vector<float> h(static_cast<size_t>(info_.hidden));
-    backend_->dev_download(h.data(), x_[last_x_], h.size() * 4);
+    backend_->dev_download(h.data(), hid_, h.size() * 4);
     return h;
 }
 
 std::vector<float> Model::last_hidden_normed() {
     const int H = info_.hidden;
-    backend_->dev_rmsnorm(x_[last_x_], output_norm_, tmp_, H, info_.eps);
+    backend_->dev_rmsnorm(hid_, output_norm_, tmp_, H, info_.eps);
     std::vector<float> h(static_cast<size_t>(H));
     backend_->dev_download(h.data(), tmp_, h.size() * 4);
     return h;
@@ -641,10 +646,9 @@ void Model::prefill_batched(size_t start, size_t count, std::vector<float>* logi
                 b.dev_download(logits->data() + at, pf_logits_, static_cast<size_t>(n) * V * 4);
             }
             if (p0 + T == count) {
-                // the last position's residual, as a decode step leaves it (last_hidden)
-                b.dev_fill(x_[0], 0.f, H);
-                b.dev_add(x_[0], pf_x_ + static_cast<uint64_t>(T - 1) * H * 4, static_cast<int>(H));
-                last_x_ = 0;
+                // the last position's residual, as a decode step with logits leaves it
+                b.dev_fill(hid_, 0.f, H);
+                b.dev_add(hid_, pf_x_ + static_cast<uint64_t>(T - 1) * H * 4, static_cast<int>(H));
             }
         }
     }

@@ -98,7 +98,7 @@ private:
     emprise_weight embd_ = 0, output_ = 0, output_norm_ = 0;
     emprise_dev x_[2] = {0, 0}, delta_attn_ = 0, delta_ffn_ = 0, norm_ = 0, tmp_ = 0, qkv_ = 0, attn_out_ = 0, logits_ = 0;
     emprise_dev dev_state_ = 0, dev_next_ = 0, dev_prompt_ = 0, dev_history_ = 0;
-    int last_x_ = 0;  // residual buffer holding the stream after the last step
+    emprise_dev hid_ = 0;  // the stream after the last position evaluated with logits
     emprise_trace_fn trace_fn_ = nullptr;
     void* trace_user_ = nullptr;
     size_t position_ = 0;

@@ -104,7 +104,8 @@ emprise_status emprise_model_set_trace(emprise_model* m, emprise_trace_fn fn, vo
  * replayed steps, the last as a decode step -- and writes the last position's logits
  * (vocab floats; may be NULL). The reference prefills in chunks of 4 positions. */
 emprise_status emprise_model_prefill(emprise_model* m, const int* tokens, size_t n, float* logits);
-/* The residual stream after the last evaluated position (Model::last_hidden_raw). */
+/* The residual stream after the last position evaluated with logits (Model::last_hidden_raw;
+   model.cpp:247-251 keeps it only there: positions evaluated without logits leave it). */
 emprise_status emprise_model_last_hidden(emprise_model* m, float* hidden);
 /* Model::last_hidden (model.cpp:483): that residual through the output norm. */
 emprise_status emprise_model_last_hidden_normed(emprise_model* m, float* hidden);

@@ -91,6 +91,54 @@ def ref_available() -> bool:
     return REF_LIB.exists()
 
 
+REF_MODEL_LIB = HERE / "_ref" / "libemprise_refmodel.so"
+_refm = None
+
+
+def ref_model_available() -> bool:
+    return REF_MODEL_LIB.exists()
+
+
+def refm() -> ctypes.CDLL:
+    """The reference's own Model and Tokenizer (model.cpp, tokenizer.cpp, ...) over a C
+    ABI (ref_model_shim.cpp), on its CPU backend."""
+    global _refm
+    if _refm is None:
+        if not REF_MODEL_LIB.exists():
+            raise RuntimeError(f"{REF_MODEL_LIB} missing (built only where the reference tree is mounted)")
+        R = ctypes.CDLL(str(REF_MODEL_LIB))
+        vp, u64, i32, i64 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int64
+        R.refm_last_error.restype = ctypes.c_char_p
+        R.refm_open.restype = vp
+        R.refm_open.argtypes = [ctypes.c_char_p, u64, ctypes.c_uint]
+        R.refm_close.argtypes = [vp]
+        R.refm_set_trace.argtypes = [vp, TRACE_FN, vp]
+        R.refm_reset.restype = i32
+        R.refm_reset.argtypes = [vp]
+        R.refm_evaluate.restype = i32
+        R.refm_evaluate.argtypes = [vp, i32, _fp, u64]
+        R.refm_evaluate_block.restype = i32
+        R.refm_evaluate_block.argtypes = [vp, ctypes.POINTER(ctypes.c_int), u64, _fp, u64]
+        R.refm_prefill.restype = i32
+        R.refm_prefill.argtypes = [vp, ctypes.POINTER(ctypes.c_int), u64, _fp, u64]
+        R.refm_last_hidden.restype = i32
+        R.refm_last_hidden.argtypes = [vp, i32, _fp, u64]
+        R.refm_mtp_draft.restype = i32
+        R.refm_mtp_draft.argtypes = [vp, _fp, u64, i32, u64, _fp, u64]
+        R.refm_mtp_hidden.restype = i32
+        R.refm_mtp_hidden.argtypes = [vp, _fp, u64]
+        R.refm_reset_mtp.restype = i32
+        R.refm_reset_mtp.argtypes = [vp]
+        R.refm_encode.restype = i64
+        R.refm_encode.argtypes = [vp, ctypes.c_char_p, u64, i32, ctypes.POINTER(ctypes.c_int), u64]
+        R.refm_decode.restype = i64
+        R.refm_decode.argtypes = [vp, i32, ctypes.c_char_p, u64]
+        R.refm_chat_prompt.restype = i64
+        R.refm_chat_prompt.argtypes = [vp, ctypes.c_char_p, u64, ctypes.c_char_p, u64]
+        _refm = R
+    return _refm
+
+
 def ref() -> ctypes.CDLL:
     global _ref
     if _ref is None:
@@ -296,3 +344,99 @@ class Model:
         if n < 0:
             raise RuntimeError(lib().eo_last_error().decode())
         return list(toks[:n]), margins[:n].copy()
+
+
+class RefModel:
+    """The reference's own emprise::Model (CPU backend) over a GGUF file, for pinning the
+    oracle's model composition and tokenizer; the same method names as Model above."""
+
+    def __init__(self, path: str, context: int = 4096, threads: int = 0):
+        self.m = refm().refm_open(str(path).encode(), context, threads)
+        if not self.m:
+            raise RuntimeError(refm().refm_last_error().decode())
+        probe = Model(path, context=8)
+        self.vocab, self.hidden = probe.vocab, probe.hidden
+        probe.close()
+        self._trace = None
+
+    def close(self):
+        if self.m:
+            refm().refm_close(self.m)
+            self.m = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc:
+            raise RuntimeError(refm().refm_last_error().decode())
+
+    def set_trace(self, store):
+        self._trace = trace_recorder(store) if store is not None else None
+        refm().refm_set_trace(self.m, self._trace if self._trace else TRACE_FN(), None)
+
+    def reset(self):
+        self._check(refm().refm_reset(self.m))
+
+    def evaluate(self, token: int, logits: bool = True):
+        out = np.empty(self.vocab, dtype=np.float32) if logits else None
+        self._check(refm().refm_evaluate(self.m, token, _f(out) if logits else None, self.vocab))
+        return out
+
+    def evaluate_block(self, tokens):
+        out = np.empty((len(tokens), self.vocab), dtype=np.float32)
+        t = (ctypes.c_int * len(tokens))(*tokens)
+        self._check(refm().refm_evaluate_block(self.m, t, len(tokens), _f(out), self.vocab))
+        return out
+
+    def prefill(self, tokens):
+        out = np.empty(self.vocab, dtype=np.float32)
+        t = (ctypes.c_int * len(tokens))(*tokens)
+        self._check(refm().refm_prefill(self.m, t, len(tokens), _f(out), self.vocab))
+        return out
+
+    def last_hidden(self, normed: bool = False) -> np.ndarray:
+        out = np.empty(self.hidden, dtype=np.float32)
+        self._check(refm().refm_last_hidden(self.m, 0 if normed else 1, _f(out), self.hidden))
+        return out
+
+    def mtp_draft(self, hidden, token: int, position: int):
+        h = np.ascontiguousarray(hidden, dtype=np.float32)
+        out = np.empty(self.vocab, dtype=np.float32)
+        self._check(refm().refm_mtp_draft(self.m, _f(h), h.size, token, position, _f(out), self.vocab))
+        return out
+
+    def mtp_hidden(self):
+        out = np.empty(self.hidden, dtype=np.float32)
+        self._check(refm().refm_mtp_hidden(self.m, _f(out), self.hidden))
+        return out
+
+    def reset_mtp(self):
+        self._check(refm().refm_reset_mtp(self.m))
+
+    def encode(self, text: str, parse_special: bool = True):
+        b = text.encode()
+        cap = 4 * len(b) + 16
+        ids = (ctypes.c_int * cap)()
+        n = refm().refm_encode(self.m, b, len(b), 1 if parse_special else 0, ids, cap)
+        if n < 0:
+            raise RuntimeError(refm().refm_last_error().decode())
+        return list(ids[:n])
+
+    def decode(self, token: int) -> bytes:
+        buf = ctypes.create_string_buffer(256)
+        n = refm().refm_decode(self.m, token, buf, 256)
+        if n < 0:
+            raise RuntimeError(refm().refm_last_error().decode())
+        return buf.raw[:n]
+
+    def chat_prompt(self, user: str) -> str:
+        b = user.encode()
+        buf = ctypes.create_string_buffer(len(b) + 256)
+        n = refm().refm_chat_prompt(self.m, b, len(b), buf, len(buf))
+        if n < 0:
+            raise RuntimeError(refm().refm_last_error().decode())
+        return buf.raw[:n].decode()

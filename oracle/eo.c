@@ -866,8 +866,9 @@ int eo_model_evaluate(eo_model* m, int token, float* logits) {
         trace_point(m, "l_out", l, x, (size_t)H);
     }
     if (rc == 0) {
-        memcpy(m->last_hidden, x, (size_t)H * sizeof(float));
         if (logits) {
+            /* the hidden vectors are kept from positions with logits only (model.cpp:247-251) */
+            memcpy(m->last_hidden, x, (size_t)H * sizeof(float));
             eo_rms(x, (size_t)H, m->output_norm, m->eps);
             trace_point(m, "result_norm", -1, x, (size_t)H);
             rc = mlinear(m, m->toutput, m->output, x, (size_t)H, logits, (size_t)m->vocab);
@@ -1005,8 +1006,8 @@ int eo_model_evaluate_many(eo_model* m, const int* tokens, size_t n, float* logi
     }
     if (rc == 0) {
         float* last = x + (n - 1) * H;
-        memcpy(m->last_hidden, last, H * sizeof(float));
         if (logits) {
+            memcpy(m->last_hidden, last, H * sizeof(float));
             eo_rms(last, H, m->output_norm, m->eps);
             rc = mlinear(m, m->toutput, m->output, last, H, logits, (size_t)m->vocab);
         }

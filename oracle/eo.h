@@ -25,13 +25,16 @@
  *   eo_attention       invariants: L=1 gives v*sigmoid(gate), equal keys give the mean
  *                      of v, fp64 brute force
  *   eo_model_*         composition of the above; teacher-forced token agreement
- *                      with a step-by-step composition of _ref ops
+ *                      with a step-by-step composition of _ref ops; bit-equal to the
+ *                      reference's own compiled Model (_ref/libemprise_refmodel.so) on
+ *                      every traced tensor, logits, hidden vectors, evaluate_block, prefill
  *   eo_quantize_q8     core.cpp:119-125's construction of the checked input; fp16(s) by
  *                      the test's monotone search (core.cpp:14-21), tested against numpy's
  *                      float16 rounding and the GPU's standalone quantiser bit for bit
  *   eo_model_evaluate_many  bit-equal to eo_model_evaluate position by position (logits,
  *                      last residual, the state left behind), plain and Q8
- *   eo_model_mtp_*     closed forms on F32 models built for them: each half of the
+ *   eo_model_mtp_*     bit-equal to the reference's Model::mtp_draft/mtp_hidden; and
+ *                      closed forms on F32 models built for them: each half of the
  *                      [enorm(e) | hnorm(h)] input, the one-row attention (v times the
  *                      sigmoid gate), the FFN, the head; cache growth and reset
  *   eo_model_last_hidden_normed  the output norm of eo_model_last_hidden
@@ -117,7 +120,8 @@ int eo_model_seek(eo_model* m, size_t position);
  * margins (optional) gets the top-1 minus top-2 logit gap for each emitted token. */
 int eo_model_generate(eo_model* m, const int* prompt, size_t prompt_len, size_t count,
                       int* tokens, float* margins);
-/* Layer trace of the last evaluate: the residual after layer `layer` (l_out). */
+/* The residual stream after the last position evaluated with logits
+ * (Model::last_hidden_raw; model.cpp:247-251 updates it only there). */
 int eo_model_last_hidden(const eo_model* m, float* out);
 /* Model::last_hidden (model.cpp:483): that residual through the output norm. */
 int eo_model_last_hidden_normed(const eo_model* m, float* out);

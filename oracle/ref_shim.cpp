@@ -2,8 +2,8 @@
 // backend.cpp from /root/reference/v1.1/src), compiled unchanged into
 // oracle/_ref/libemprise_ref.so by oracle/Makefile. TEST INFRASTRUCTURE ONLY: used by
 // tests/ to pin the oracle restatement against the reference's compiled code.
-// model.cpp is not built here: it pulls in tokenizer.cpp, which needs PCRE2's
-// configure-generated headers.
+// The reference's Model and Tokenizer are wrapped by ref_model_shim.cpp in a library of
+// their own (libemprise_refmodel.so, with PCRE2 and utf8proc).
 #include "emprise/backend.hpp"
 #include "emprise/gguf.hpp"
 

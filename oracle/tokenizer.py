@@ -8,9 +8,11 @@ The pre-tokenizer is the reference's PCRE2 pattern (tokenizer.cpp:112) run by th
 `regex` module, with \\s spelled out as PCRE2's UCP space (\\p{Z} plus \\h and \\v:
 U+0009-000D, U+0085, U+180E), which is not exactly `regex`'s own \\s. The merge loop,
 special-token search, byte encoder and decode table follow tokenizer.cpp:25-52, :60-105
-and :114-139 step by step. Pinned by tests/test_tokenizer.py against the HF `tokenizers`
-library (an independent byte-level BPE) on the same vocabulary and merges, by the
-byte round trip, and by pre-tokenizer splits derived by hand from the pattern.
+and :114-139 step by step. Pinned by tests/test_oracle_refmodel.py against the
+reference's own compiled tokenizer.cpp (where oracle/_ref is built), by
+tests/test_tokenizer.py against the HF `tokenizers` library (an independent byte-level
+BPE) on the same vocabulary and merges, by the byte round trip, and by pre-tokenizer
+splits derived by hand from the pattern.
 """
 import struct
 

@@ -128,8 +128,9 @@ def test_matvec_rejects_mismatched_sizes():
 def test_oracle_trace_points_report_the_model_tensors(tmp_path):
     """The oracle's trace hook (model.cpp:118-120) reports, per position, attn_norm-L,
     attn_residual-L and l_out-L for every layer, then result_norm and logits when logits
-    are asked for; the last l_out is the residual the model keeps (last_hidden), the
-    result_norm its normed form and the logits trace the returned logits, bit for bit."""
+    are asked for; the last l_out of a position with logits is the residual the model
+    keeps (last_hidden, left as it was by a position without), the result_norm its normed
+    form and the logits trace the returned logits, bit for bit."""
     import oracle
     from emprise_amd import TINY, synth_write
     p = tmp_path / "tiny.gguf"
@@ -148,7 +149,9 @@ def test_oracle_trace_points_report_the_model_tensors(tmp_path):
             assert np.array_equal(store[f"{pos}.logits"], out)
             assert np.array_equal(store[f"{pos}.result_norm"], m.last_hidden(normed=True))
         assert new == names
-        assert np.array_equal(store[f"{pos}.l_out-{L - 1}"], m.last_hidden())
+        # the hidden vectors are kept from positions with logits only (model.cpp:247-251)
+        keep = pos if want_logits else pos - 1
+        assert np.array_equal(store[f"{keep}.l_out-{L - 1}"], m.last_hidden())
     m.set_trace(None)
     m.evaluate(1, True)
     assert not any(k.startswith("3.") for k in store)
