@@ -14,7 +14,12 @@
 // sigmoid output gate. (A last-workgroup merge inside the first kernel needs
 // agent-scope fences, which write back and invalidate an L2 on this part: measured
 // 29.3 us per call at 512 positions against 9.9 us for the two kernels, and 2.9 us more
-// even at 16 positions, where four workgroups take part.)
+// even at 16 positions, where four workgroups take part. Without fences -- partials
+// written with agent-scope atomic stores, s_waitcnt 0 and a barrier before a relaxed
+// ticket, the last range of each KV head merging with agent-scope loads -- it is
+// correct and still slower past a few ranges, one workgroup reading every partial:
+// 8.3 / 9.7 / 17.3 / 26.6 / 31.9 us at 16 / 100 / 512 / 1024 / 4096 positions against
+// 8.7 / 8.6 / 9.0 / 9.5 / 15.6 us for the two kernels, 569 against 592 tok/s.)
 //
 // Inside a workgroup (8 waves) every wave owns kAttnSub/8 positions of each sub-chunk
 // and keeps their K and V rows in registers, lane l holding dims E*l .. E*l+E-1 (head_dim = 64*E,
