@@ -80,6 +80,7 @@ def hip_lib() -> ctypes.CDLL:
         "emprise_hip_upload": (st, [vp, u64, vp, ctypes.c_size_t]),
         "emprise_hip_download": (st, [vp, vp, u64, ctypes.c_size_t]),
         "emprise_hip_fill": (st, [vp, u64, f32, ctypes.c_size_t]),
+        "emprise_hip_stream_read": (st, [vp, u64, u64, u64]),
         "emprise_hip_upload_weight": (st, [vp, ctypes.c_uint32, u64, u64, vp, ctypes.c_size_t, P(u64)]),
         "emprise_hip_weight_free": (st, [vp, u64]),
         "emprise_hip_weight_data": (u64, [vp, u64]),
@@ -228,6 +229,11 @@ class HipBackend:
 
     def fill(self, dst: int, value: float, n: int):
         self._check(self.lib.emprise_hip_fill(self.h, dst, value, n))
+
+    def stream_read(self, src: int, nbytes: int, sink: int):
+        """Reads nbytes (a multiple of 4 KiB) as a plain non-temporal stream; sink takes
+        one word per workgroup (4096 uint32): the achievable-read-bandwidth probe."""
+        self._check(self.lib.emprise_hip_stream_read(self.h, src, nbytes, sink))
 
     # weights
     def upload_weight(self, wtype: int, cols: int, rows: int, data) -> int:

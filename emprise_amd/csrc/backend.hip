@@ -405,6 +405,14 @@ emprise_status emprise_hip_fill(emprise_hip* h, emprise_dev dst, float value, si
     return traced(h, "fill", n * 4, [&] { return launch_fill(reinterpret_cast<float*>(dst), value, n, h->stream); });
 }
 
+emprise_status emprise_hip_stream_read(emprise_hip* h, emprise_dev src, uint64_t bytes, emprise_dev sink) {
+    if (!h || !src || !sink) return fail(EMPRISE_EINVAL, "null argument");
+    if (!bytes || bytes % 4096) return fail(EMPRISE_EINVAL, "stream_read: bytes must be a positive multiple of 4 KiB");
+    return traced(h, "stream_read", bytes, [&] {
+        return launch_stream_read(reinterpret_cast<const void*>(src), bytes, reinterpret_cast<uint32_t*>(sink), h->stream);
+    });
+}
+
 emprise_status emprise_hip_upload_weight(emprise_hip* h, uint32_t type, uint64_t cols, uint64_t rows, const void* data,
                                          size_t len, emprise_weight* out) {
     if (!h || !data || !out) return fail(EMPRISE_EINVAL, "null argument");

@@ -227,6 +227,7 @@ hipError_t launch_rope_table(float2* table, int context, int rotary, float base,
 
 // ---- small ops ----
 hipError_t launch_fill(float* dst, float value, size_t n, hipStream_t stream);
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream);
 hipError_t launch_fill_u64(unsigned long long* dst, unsigned long long value, size_t n, hipStream_t stream);
 hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t stream);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int n, int rows, float eps,

@@ -70,6 +70,12 @@ emprise_status emprise_hip_upload(emprise_hip* h, emprise_dev dst, const void* s
 emprise_status emprise_hip_download(emprise_hip* h, void* dst, emprise_dev src, size_t bytes);      /* dev_download */
 /* Fills n floats with value on the stream (graph-safe: a kernel, not a memset). */
 emprise_status emprise_hip_fill(emprise_hip* h, emprise_dev dst, float value, size_t n);
+/* Measurement aid; no counterpart in the reference. Reads `bytes` (a multiple of 4 KiB)
+ * from src with non-temporal 16-byte loads (one 8-wave workgroup per CU, each wave one
+ * 4 KiB piece at a time) and writes one word per workgroup (the XOR of what it read) to
+ * sink (4096 uint32). Its rate is the achievable HBM read bandwidth bench.py reports the
+ * decode against. */
+emprise_status emprise_hip_stream_read(emprise_hip* h, emprise_dev src, uint64_t bytes, emprise_dev sink);
 
 /* ---- weights ---------------------------------------------------------------------- */
 

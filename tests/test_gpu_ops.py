@@ -491,3 +491,23 @@ def test_graph_replay_matches_eager(backend):
         assert backend.download(idx, 1, np.int32)[0] == eager_i[0]
     backend.graph_destroy(g)
     backend.weight_free(w)
+
+
+def test_stream_read_sees_every_word(backend):
+    """The read-bandwidth probe (bench.py's achievable-HBM figure) reads every byte: the
+    XOR of its per-workgroup words is the XOR of the buffer, for a buffer of more 4 KiB
+    pieces than waves (several pieces each) and one of fewer; sizes that are not whole
+    pieces are refused."""
+    rng = np.random.default_rng(11)
+    sink = backend.alloc(4096 * 4)
+    for pieces in (3000, 5):
+        data = rng.integers(0, 2**32, size=pieces * 4096, dtype=np.uint32)
+        src = backend.to_device(data)
+        backend.fill(sink, 0.0, 4096)
+        backend.stream_read(src, data.nbytes, sink)
+        words = backend.download(sink, (4096,), np.uint32)
+        assert np.bitwise_xor.reduce(words) == np.bitwise_xor.reduce(data), pieces
+        with pytest.raises(InvalidArgument):
+            backend.stream_read(src, data.nbytes - 4, sink)
+        backend.free(src)
+    backend.free(sink)
