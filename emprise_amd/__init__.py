@@ -645,8 +645,8 @@ class Model:
         attn_residual-L, l_out-L, result_norm, logits), with a copy of the tensor; None
         removes it."""
         if hook is None:
-            self._trace = None
             _host_check(host_lib().emprise_model_set_trace(self.m, TRACE_FN(), None))
+            self._trace = None  # released only once the library no longer holds it
             return
 
         def tramp(_user, position, name, data, n):

@@ -287,8 +287,9 @@ class Model:
     def set_trace(self, store):
         """ModelOptions::trace: every tensor evaluate() passes the hook is kept in `store`
         (see trace_recorder); None removes the hook."""
-        self._trace = trace_recorder(store) if store is not None else None
-        lib().eo_model_set_trace(self.m, self._trace if self._trace else TRACE_FN(), None)
+        hook = trace_recorder(store) if store is not None else None
+        lib().eo_model_set_trace(self.m, hook if hook else TRACE_FN(), None)
+        self._trace = hook  # the previous hook is released only once the library holds the new one
 
     def evaluate(self, token: int, logits: bool = True):
         out = np.empty(self.vocab, dtype=np.float32) if logits else None
@@ -375,8 +376,9 @@ class RefModel:
             raise RuntimeError(refm().refm_last_error().decode())
 
     def set_trace(self, store):
-        self._trace = trace_recorder(store) if store is not None else None
-        refm().refm_set_trace(self.m, self._trace if self._trace else TRACE_FN(), None)
+        hook = trace_recorder(store) if store is not None else None
+        refm().refm_set_trace(self.m, hook if hook else TRACE_FN(), None)
+        self._trace = hook
 
     def reset(self):
         self._check(refm().refm_reset(self.m))
