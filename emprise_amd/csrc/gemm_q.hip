@@ -6,10 +6,11 @@
 //
 // - Weights. A Q6_K element is d * sc * (q - 32) with q a 6-bit code and sc an int8 unit
 //   scale (quant.cpp:25-40); v = sc * (q - 32) is an integer of at most 13 bits, written
-//   as v = vh + vl with vh = v truncated to fp16's 11 significant bits and vl = v - vh
-//   (|vl| <= 1): both exact fp16. A Q4_K element is (d * sc) * q - dmin * m
-//   (quant.cpp:41-61); v = sc * q is at most 63 * 15 = 945, exact in fp16 as it stands.
-//   The block scales d (and dmin) of each 256 columns are applied in FP32 once per block.
+//   as v = vh + vl with vh = v rounded to fp16 and vl = v - vh (|vl| <= 1): both exact
+//   fp16. A Q4_K element is (d * sc) * q - dmin * m (quant.cpp:41-61); v = sc * q is at
+//   most 63 * 15 = 945, exact in fp16 as it stands. The block scales d (and dmin) of each
+//   256 columns are applied in FP32 once per block. The staging waves decode in packed
+//   fp16 arithmetic, every step exact (below).
 // - Activations. Row m of X is scaled by a power of two 2^-e_m (exact) so that its largest
 //   magnitude lies in [1, 2) -- no fp16 overflow whatever the activations -- and split
 //   into xh = fp16(x) and xl = fp16(x - xh), which carry x to 22 significant bits.
@@ -45,10 +46,6 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int QM = 128, QN = 128, QKS = 64, QROW = QKS + 8;  // LDS rows padded to 144 bytes
 constexpr int QThreads = 512;
-
-__device__ __forceinline__ uint32_t pack_rtz(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
-}
 
 // Loads through global-address-space pointers (global_load_*, counted by vmcnt only).
 #define QGLOBAL __attribute__((address_space(1)))
@@ -199,24 +196,35 @@ template <> struct QRaw<kQ4K> {
     uint32_t dd;  // fp16 d | fp16 dmin << 16
 };
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Two code bytes (bytes 0, 1 of w, or 2, 3 with hi) as the fp16 pair 1024 + q: each byte
+// under an exponent byte 0x64 (v_perm_b32), which makes 1024 + q exact for q < 1024.
+__device__ __forceinline__ half2v codes_1024(uint32_t w, bool hi) {
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, w, hi ? 0x04030402u : 0x04010400u));
+}
+
 // Q6_K unit -> fp16 pieces: codes 0..3 in the low 6 bits of word d0, 4..7 of d1, 8..11 of
-// d2, 12..15 gathered from their top two bits; v = sc * (q - 32), exact in FP32, vh = v
-// with its significand cut to fp16's 11 bits, vl = v - vh.
+// d2, 12..15 gathered from their top two bits. In packed fp16 arithmetic, each step exact:
+// q - 32 = (1024 + q) - 1056; vh = fp16(v), v = sc * (q - 32); vl = fma(q - 32, sc, -vh),
+// a small integer (|vl| <= 1). Two weights per instruction, about half the instructions
+// of the same split in FP32.
 __device__ __forceinline__ void q6_unit_f16(uint32_t d0, uint32_t d1, uint32_t d2, int sc, _Float16* dh,
                                             _Float16* dl) {
     const uint32_t w[4] = {d0 & 0x3F3F3F3Fu, d1 & 0x3F3F3F3Fu, d2 & 0x3F3F3F3Fu,
                            ((d0 >> 6) & 0x03030303u) | ((d1 >> 4) & 0x0C0C0C0Cu) | ((d2 >> 2) & 0x30303030u)};
-    const float scf = (float)sc, zp = -32.f * scf;
+    const _Float16 s16 = (_Float16)(float)sc;
+    const half2v sc2 = {s16, s16}, off = {(_Float16)-1056.f, (_Float16)-1056.f};
     uint32_t hi[8], lo[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const float v0 = fmaf(ubyte_f(w[k], 2 * h), scf, zp), v1 = fmaf(ubyte_f(w[k], 2 * h + 1), scf, zp);
-            const float h0 = __uint_as_float(__float_as_uint(v0) & 0xFFFFE000u);
-            const float h1 = __uint_as_float(__float_as_uint(v1) & 0xFFFFE000u);
-            hi[2 * k + h] = pack_rtz(h0, h1);
-            lo[2 * k + h] = pack_rtz(v0 - h0, v1 - h1);
+            const half2v q = codes_1024(w[k], h) + off;
+            const half2v vh = q * sc2;
+            const half2v vl = __builtin_elementwise_fma(q, sc2, -vh);
+            hi[2 * k + h] = __builtin_bit_cast(uint32_t, vh);
+            lo[2 * k + h] = __builtin_bit_cast(uint32_t, vl);
         }
     }
     *reinterpret_cast<uint4*>(dh) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
@@ -338,14 +346,20 @@ __global__ __launch_bounds__(QThreads) void gemm_q16_kernel(QGemmArgs a) {
                 const uint32_t b = (rb.s2 >> (8 * ph)) & 0xffu;
                 const float scf = (float)(b & 63u);
                 const uint32_t wv[4] = {rb.q.x, rb.q.y, rb.q.z, rb.q.w};
+                // v = (1024 + q) * sc - 1024 * sc in one fused step: exact, the product below
+                // 1039 * 63 < 65504 and the result at most 945
+                const _Float16 s16 = (_Float16)scf;
+                const half2v sc2 = {s16, s16}, base = {(_Float16)(-1024.f * scf), (_Float16)(-1024.f * scf)};
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
                     uint32_t pk[8];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         const uint32_t nib = (wv[k] >> (4 * hf)) & 0x0F0F0F0Fu;
-                        pk[2 * k] = pack_rtz(ubyte_f(nib, 0) * scf, ubyte_f(nib, 1) * scf);
-                        pk[2 * k + 1] = pack_rtz(ubyte_f(nib, 2) * scf, ubyte_f(nib, 3) * scf);
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+                            pk[2 * k + h] = __builtin_bit_cast(
+                                uint32_t, __builtin_elementwise_fma(codes_1024(nib, h), sc2, base));
                     }
                     _Float16* dh = &Bs[buf][0][pr][32 * ph + 16 * hf];
                     *reinterpret_cast<uint4*>(dh) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
