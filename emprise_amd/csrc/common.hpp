@@ -86,6 +86,33 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return t;
 }
 
+// The Q8 codes of a block's values v for its scale s (quantize_x, cuda.cpp:547-559):
+// round(v / s), ties away from zero, with v / s the correctly rounded IEEE quotient. With y = 1 / s
+// (itself correctly rounded, once per block) the quotient comes from Markstein's
+// correction instead of a division per value: q = v*y, r = v - q*s (exact, one fused
+// multiply-add), v/s = q + r*y rounded once -- the correctly rounded quotient whenever s
+// and 1/s are normal (P. Markstein, "Computation of elementary functions on the IBM RISC
+// System/6000 processor", IBM J. Res. Dev. 34(1), 1990; J.-M. Muller et al., Handbook of
+// Floating-Point Arithmetic, the theorem on the correction step of division). Scales
+// below 2^-125 take the division itself.
+template <int N>
+__device__ __forceinline__ void q8_codes(const float (&v)[N], float s, int (&q)[N]) {
+    float t[N];
+    if (s >= 0x1p-125f) {  // one branch per block: every value takes the same path
+        const float y = 1.f / s;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const float c = v[i] * y;
+            t[i] = fmaf(fmaf(-c, s, v[i]), y, c);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) t[i] = s != 0.f ? v[i] / s : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = (int)roundf(t[i]);
+}
+
 // Numerically stable forms used by the reference (backend.cpp:10-12, cuda.cpp:414-416).
 __device__ __forceinline__ float sigmoidf_(float x) {
     return x >= 0.f ? 1.f / (1.f + expf(-x)) : expf(x) / (1.f + expf(x));

@@ -70,10 +70,17 @@ __device__ void stage_q8(int n, const float* xs, int8_t* xq, float* xscale, int*
         for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(xs[blk * 32 + i]));
         const float s = amax / 127.f;
         int s0 = 0, s1 = 0;
-        for (int i = 0; i < 32; ++i) {
-            const int q = s != 0.f ? (int)roundf(xs[blk * 32 + i] / s) : 0;
-            xq[blk * 32 + i] = (int8_t)q;
-            if (i < 16) s0 += q; else s1 += q;
+        for (int h = 0; h < 4; ++h) {
+            float v[8];
+            int q[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = xs[blk * 32 + 8 * h + i];
+            q8_codes<8>(v, s, q);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                xq[blk * 32 + 8 * h + i] = (int8_t)q[i];
+                if (h < 2) s0 += q[i]; else s1 += q[i];
+            }
         }
         xscale[blk] = half_bits_to_float(float_to_half_bits(s));
         qsum[blk * 2] = s0;
@@ -437,11 +444,9 @@ __device__ void sstage_q8(int n, const float* xs, int8_t* xq, float* xscale, int
         amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
         const float s = amax / 127.f;
         int q[8], part = 0;
+        q8_codes<8>(v, s, q);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            q[i] = s != 0.f ? (int)roundf(v[i] / s) : 0;
-            part += q[i];
-        }
+        for (int i = 0; i < 8; ++i) part += q[i];
         uint32_t lo = 0, hi = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -555,11 +560,13 @@ __device__ __forceinline__ void sinput_finish(const MvArgs& a, SInput<SB, DN>& s
             amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
             const float sc = amax / 127.f;
             const float vv[4] = {v.x, v.y, v.z, v.w};
+            int qq[4];
+            q8_codes<4>(vv, sc, qq);
             int part = 0;
             uint32_t packed = 0;
 #pragma unroll
             for (int c4 = 0; c4 < 4; ++c4) {
-                const int q = sc != 0.f ? (int)roundf(vv[c4] / sc) : 0;
+                const int q = qq[c4];
                 part += q;
                 packed |= (uint32_t)(q & 0xff) << (8 * c4);
             }

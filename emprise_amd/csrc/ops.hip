@@ -142,7 +142,13 @@ __global__ void quantize_q8_kernel(const float* x, int cols, int8_t* q, float* s
     float amax = 0.f;
     for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[blk * 32 + i]));
     const float s = amax / 127.f;
-    for (int i = 0; i < 32; ++i) q[blk * 32 + i] = (int8_t)(s != 0.f ? (int)roundf(x[blk * 32 + i] / s) : 0);
+    for (int h = 0; h < 4; ++h) {
+        float v[8];
+        int c[8];
+        for (int i = 0; i < 8; ++i) v[i] = x[blk * 32 + 8 * h + i];
+        q8_codes<8>(v, s, c);
+        for (int i = 0; i < 8; ++i) q[blk * 32 + 8 * h + i] = (int8_t)c[i];
+    }
     scales[blk] = half_bits_to_float(float_to_half_bits(s));
 }
 

@@ -511,3 +511,50 @@ def test_stream_read_sees_every_word(backend):
             backend.stream_read(src, data.nbytes - 4, sink)
         backend.free(src)
     backend.free(sink)
+
+
+def _q8_reference(x):
+    """quantize_x's rule in numpy: per 32 values s = amax / 127 (FP32), codes round(v / s)
+    with ties away from zero on the IEEE FP32 quotient, scale kept as fp16(s)."""
+    blocks = x.reshape(-1, 32)
+    s = (np.max(np.abs(blocks), axis=1) / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = (blocks / s[:, None]).astype(np.float32)
+    q = np.where(np.abs(r - np.trunc(r)) == 0.5, np.trunc(r) + np.sign(r), np.round(r))
+    q = np.where(s[:, None] == 0, 0, q).astype(np.int8).reshape(-1)
+    return q, s.astype(np.float16).astype(np.float32)
+
+
+def test_quantize_q8_exact_on_ties_and_scales(backend):
+    """The quantiser's quotient v / s (computed from one reciprocal per block and a
+    correction step, not a division per value) equals the IEEE quotient: blocks whose scale
+    is a power of two with values exactly on every half-integer code boundary (ties away
+    from zero), their FP32 neighbours on both sides, random blocks over scales from 1e-30
+    to 1e30, a block whose scale is below 2^-125 (the per-value division path) and a zero
+    block; codes and kept scales equal numpy's bit for bit."""
+    rng = np.random.default_rng(17)
+    blocks = []
+    for e in range(-40, 41, 5):  # s = 2^e exactly: amax = 127 * 2^e
+        base = np.float32(2.0 ** e)
+        for lo in range(-127, 127, 31):
+            ties = (np.arange(lo, lo + 31, dtype=np.float64) + 0.5) * float(base)
+            b = np.concatenate([[127 * float(base)], ties]).astype(np.float32)
+            blocks += [b, np.nextafter(b, np.float32(np.inf)), np.nextafter(b, np.float32(-np.inf))]
+            blocks[-2][0] = blocks[-1][0] = b[0]  # keep amax, so s stays 2^e
+    for mag in (1e-30, 1e-12, 1e-3, 1.0, 7.5, 1e6, 1e30):
+        blocks += list((rng.standard_normal((64, 32)) * mag).astype(np.float32))
+    tiny = (rng.uniform(-1, 1, 32) * 2e-36).astype(np.float32)  # s ~ 1.6e-38 < 2^-125: the division path
+    tiny[5] = np.float32(2e-36)
+    blocks += [tiny, np.zeros(32, np.float32)]
+    x = np.concatenate(blocks).astype(np.float32)
+    n = x.size
+    xd, qd, sd = backend.to_device(x), backend.alloc(n), backend.alloc(n // 32 * 4)
+    backend.quantize_q8(xd, n, qd, sd)
+    q = backend.download(qd, n, np.int8)
+    s = backend.download(sd, n // 32)
+    q_ref, s_ref = _q8_reference(x)
+    bad = np.nonzero(q != q_ref)[0]
+    assert bad.size == 0, f"{bad.size} codes differ, first at {bad[0]}: x {x[bad[0]]!r} got {q[bad[0]]} want {q_ref[bad[0]]}"
+    assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+    for b in (xd, qd, sd):
+        backend.free(b)
